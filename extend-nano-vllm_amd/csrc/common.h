@@ -1,0 +1,91 @@
+// Shared device helpers for the EAGLE3 speculative-step kernels (gfx950).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "nanovllm_amd.h"
+
+namespace nva {
+
+typedef __attribute__((__vector_size__(8 * sizeof(short)))) short bf16x8_t;
+typedef __attribute__((__vector_size__(4 * sizeof(short)))) short bf16x4_t;
+typedef __attribute__((__vector_size__(4 * sizeof(float)))) float f32x4_t;
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- bf16
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t b) {
+  return __uint_as_float(static_cast<uint32_t>(b) << 16);
+}
+
+// Round-to-nearest-even float -> bf16, NaN -> 0x7FC0 (the conversion torch
+// applies when it stores a float result as bfloat16).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0;
+  uint32_t bias = ((u >> 16) & 1u) + 0x7FFFu;
+  return static_cast<uint16_t>((u + bias) >> 16);
+}
+
+// ---------------------------------------------------------------- fp8 e4m3fn
+
+// OCP float8_e4m3fn -> float.  The byte shifted left by 7 is an IEEE half with
+// the same sign/mantissa and an exponent bias of 15 instead of 7, so the half
+// value times 2^8 is exact for normals and subnormals alike.  0x7F/0xFF are NaN.
+__device__ __forceinline__ float e4m3_to_f32(uint32_t b) {
+  uint32_t em = b & 0x7Fu;
+  uint16_t hbits = static_cast<uint16_t>(((b & 0x80u) << 8) | (em << 7));
+  _Float16 h = __builtin_bit_cast(_Float16, hbits);
+  float v = static_cast<float>(h) * 256.0f;
+  return em == 0x7Fu ? __builtin_nanf("") : v;
+}
+
+// float -> float8_e4m3fn, round to nearest even, magnitudes >= 464 (including
+// infinities) saturate to +-448, NaN -> 0x7F with the sign kept.
+__device__ __forceinline__ uint32_t f32_to_e4m3(float x) {
+  uint32_t u = __float_as_uint(x);
+  uint32_t sign = (u >> 24) & 0x80u;
+  uint32_t a = u & 0x7FFFFFFFu;
+  if (a > 0x7F800000u) return sign | 0x7Fu;
+  float af = __uint_as_float(a);
+  if (af >= 464.0f) return sign | 0x7Eu;
+  if (af < 0.015625f) {                       // below the smallest normal 2^-6
+    // subnormal codes are m * 2^-9, m = 0..7; m == 8 is the code of 2^-6
+    uint32_t m = static_cast<uint32_t>(__builtin_rintf(af * 512.0f));
+    return sign | m;
+  }
+  int32_t e = static_cast<int32_t>(a >> 23) - 127;   // -6 .. 8
+  uint32_t mant = a & 0x7FFFFFu;
+  uint32_t keep = mant >> 20;
+  uint32_t low = mant & 0xFFFFFu;
+  if (low > 0x80000u || (low == 0x80000u && (keep & 1u))) ++keep;
+  if (keep == 8u) { keep = 0; ++e; }
+  return sign | (static_cast<uint32_t>(e + 7) << 3) | keep;
+}
+
+// ---------------------------------------------------------------- misc
+
+__device__ __forceinline__ int wave_lane() { return threadIdx.x & (kWave - 1); }
+
+template <typename T>
+__device__ __forceinline__ T load_acquire_agent(const T* p) {
+  return __hip_atomic_load(p, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ T load_relaxed_agent(const T* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <typename T>
+__device__ __forceinline__ void store_relaxed_agent(T* p, T v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+inline int launch_status() {
+  return hipGetLastError() == hipSuccess ? NVA_OK : NVA_ERR_LAUNCH;
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+}  // namespace nva

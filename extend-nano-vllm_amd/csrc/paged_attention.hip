@@ -1,0 +1,635 @@
+// K1: paged verify attention for gfx950 (MFMA 16x16x32 bf16).
+//
+// Work decomposition: one 256-thread workgroup (4 waves) per
+// (kv split, kv head, sequence).  The query tile of a workgroup is the
+// q_i * G query rows that share the kv head (G = Hq / Hkv), padded to NT*16
+// columns (NT = 1..4).  The key range of the split is walked in 32-key chunks,
+// chunk c by wave c % 4, each wave keeping its own online-softmax state.
+//
+// Per 32-key chunk a wave computes S^T = K . Q^T (two 16-key tiles, MFMA with
+// keys as M, query rows as N, head_dim as K in four 32-wide slices) and
+// O^T += V^T . P^T (head_dim as M in eight 16-row tiles, keys as K).
+//   * The MFMA sums over K in any order, so K and Q operands only have to
+//     agree on which head_dim element sits in which lane slot: lane l holds
+//     row (l % 16) and elements 32*s + 8*(l/16) .. +7 of slice s, a 16-byte
+//     load straight from the paged cache.
+//   * The S^T accumulator layout (lane l: query column l % 16, keys
+//     4*(l/16) + i) is exactly the B-operand layout of the P^T operand once
+//     the 8 lane slots are mapped to keys {4g..4g+3, 16+4g..16+4g+3}; V^T uses
+//     the same key mapping.  V is therefore staged through a wave-private LDS
+//     tile (row pitch 68 dwords: conflict-free for the column reads) and read
+//     back two head_dim elements per dword, feeding an even and an odd d-tile.
+// FP8 caches are dequantised to bf16 on load (exact: every e4m3 value is a
+// bf16 value).  The waves' states are merged through LDS at the end; a split
+// that covers the whole sequence writes bf16 output directly, otherwise it
+// writes a normalised fp32 partial plus its log-sum-exp, and a second kernel
+// merges the splits.
+#include "common.h"
+
+namespace nva {
+namespace {
+
+constexpr int kD = 128;
+constexpr int kWaves = 4;
+constexpr int kThreads = kWaves * kWave;
+constexpr int kChunk = 32;
+constexpr int kVPitch = 68;                          // dwords per staged V row
+constexpr int kVStage = kChunk * kVPitch;            // dwords per wave
+constexpr int kAccPitch = kD + 4;                    // floats per column in the merge tile
+constexpr int kLdsDwords = kWaves * kVStage + 2 * kWaves * 64;
+static_assert(kWaves * 16 * kAccPitch <= kWaves * kVStage, "merge tile must fit the V stages");
+constexpr int kTargetWorkgroups = 2048;
+constexpr int kMinSplit = 128;
+constexpr float kLog2e = 1.4426950408889634f;
+
+struct AttnParams {
+  const uint16_t* q;
+  int64_t q_row_stride, q_head_stride;
+  const uint8_t* k_cache;
+  const uint8_t* v_cache;
+  int64_t blk_stride, tok_stride, head_stride;       // elements
+  int32_t num_blocks, block_size;
+  const int32_t* cu_q;                                // null: row i is sequence i
+  const int32_t* cu_k;                                // non-null: L_i = cu_k[i+1]-cu_k[i]
+  const int32_t* seqlens;                             // otherwise L_i = seqlens[i]
+  const int32_t* block_tables;
+  int64_t bt_stride;
+  int32_t bt_cols;
+  int32_t num_seqs, num_tokens, max_q, max_k;
+  int32_t hq, hkv, group;
+  float scale_log2;
+  const float* k_scale;
+  const float* v_scale;
+  uint16_t* out;
+  int64_t out_row_stride, out_head_stride;
+  float* ws_o;
+  float* ws_lse;
+  int32_t split_len, max_splits;
+};
+
+__device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ f32x4_t mfma(bf16x8_t a, bf16x8_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
+}
+
+// 8 fp8 bytes -> 8 bf16 (exact)
+__device__ __forceinline__ bf16x8_t fp8x8_to_bf16(uint2 w) {
+  const uint32_t in[2] = {w.x, w.y};
+  uint32_t o[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t src = in[k >> 1] >> ((k & 1) * 16);
+    const uint32_t lo = __float_as_uint(e4m3_to_f32(src & 0xFFu)) >> 16;
+    const uint32_t hi = __float_as_uint(e4m3_to_f32((src >> 8) & 0xFFu)) >> 16;
+    o[k] = lo | (hi << 16);
+  }
+  uint4 r = make_uint4(o[0], o[1], o[2], o[3]);
+  return __builtin_bit_cast(bf16x8_t, r);
+}
+
+__device__ __forceinline__ void seq_geometry(const AttnParams& p, int seq, int& q_start, int& q_len,
+                                             int& L) {
+  if (p.cu_q) {
+    q_start = p.cu_q[seq];
+    q_len = p.cu_q[seq + 1] - q_start;
+  } else {
+    q_start = seq;
+    q_len = 1;
+  }
+  q_len = q_len > p.max_q ? p.max_q : q_len;
+  if (q_start < 0 || q_start >= p.num_tokens) q_len = 0;
+  else if (q_len > p.num_tokens - q_start) q_len = p.num_tokens - q_start;
+  L = p.cu_k ? p.cu_k[seq + 1] - p.cu_k[seq] : p.seqlens[seq];
+  L = L > p.max_k ? p.max_k : L;
+}
+
+template <int NT, bool FP8>
+__global__ void __launch_bounds__(kThreads)
+paged_attention_kernel(AttnParams p) {
+  __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsDwords];
+
+  const int split = blockIdx.x;
+  const int kvh = blockIdx.y;
+  const int seq = blockIdx.z;
+  const int wave = threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int g = lane >> 4;
+  const int m16 = lane & 15;
+
+  int q_start, q_len, L;
+  seq_geometry(p, seq, q_start, q_len, L);
+  if (q_len <= 0) return;
+  const int rows = q_len * p.group;
+  const int kv_begin = split * p.split_len;
+  if (L <= 0) {
+    // nothing visible: zero output rows (once, from split 0)
+    if (split != 0) return;
+    for (int idx = threadIdx.x; idx < rows * (kD / 8); idx += kThreads) {
+      const int n = idx / (kD / 8), dv = idx % (kD / 8);
+      const int j = n / p.group, hh = n % p.group;
+      uint16_t* o = p.out + static_cast<int64_t>(q_start + j) * p.out_row_stride +
+                    static_cast<int64_t>(kvh * p.group + hh) * p.out_head_stride + dv * 8;
+      *reinterpret_cast<uint4*>(o) = make_uint4(0, 0, 0, 0);
+    }
+    return;
+  }
+  if (kv_begin >= L) return;
+  const int kv_end = kv_begin + p.split_len < L ? kv_begin + p.split_len : L;
+  const int nsplit = (L + p.split_len - 1) / p.split_len;
+
+  float kscale = 1.0f, vscale = 1.0f;
+  if (FP8) {
+    kscale = p.k_scale ? *p.k_scale : 1.0f;
+    vscale = p.v_scale ? *p.v_scale : 1.0f;
+  }
+  const float sl2 = p.scale_log2 * kscale;
+
+  // ---- query operands and causal limits for this lane's columns
+  bf16x8_t qop[NT][4];
+  int lim[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int n = nt * 16 + m16;
+    if (n < rows) {
+      const int j = n / p.group, hh = n % p.group;
+      const uint16_t* qp = p.q + static_cast<int64_t>(q_start + j) * p.q_row_stride +
+                           static_cast<int64_t>(kvh * p.group + hh) * p.q_head_stride;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) qop[nt][s] = *reinterpret_cast<const bf16x8_t*>(qp + 32 * s + 8 * g);
+      const int c = L - q_len + j;
+      lim[nt] = c < L - 1 ? c : L - 1;
+    } else {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) qop[nt][s] = bf16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
+      lim[nt] = -1;
+    }
+  }
+
+  float m_run[NT], l_run[NT];
+  f32x4_t acc[NT][8];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    m_run[nt] = -INFINITY;
+    l_run[nt] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[nt][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+
+  uint32_t* vst = lds + wave * kVStage;
+  const int nchunks = (kv_end - kv_begin + kChunk - 1) / kChunk;
+  const int32_t* bt = p.block_tables + static_cast<int64_t>(seq) * p.bt_stride;
+  const int64_t esz = FP8 ? 1 : 2;
+
+  for (int c = wave; c < nchunks; c += kWaves) {
+    const int kb = kv_begin + c * kChunk;
+    const int lblk = kb / p.block_size;
+    const int pblk = lblk < p.bt_cols ? bt[lblk] : -1;
+    if (pblk < 0 || pblk >= p.num_blocks) continue;   // empty block: keys masked
+    const int off0 = kb % p.block_size;
+    const int64_t blk_base = static_cast<int64_t>(pblk) * p.blk_stride +
+                             static_cast<int64_t>(kvh) * p.head_stride;
+
+    // ---- K operands: key (16*kt + m16), d slice s
+    bf16x8_t kop[2][4];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+      int key = kb + kt * 16 + m16;
+      key = key < L ? key : L - 1;
+      const int64_t e = blk_base + static_cast<int64_t>(off0 + key - kb) * p.tok_stride;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        if (FP8) {
+          const uint2 w = *reinterpret_cast<const uint2*>(p.k_cache + (e + 32 * s + 8 * g));
+          kop[kt][s] = fp8x8_to_bf16(w);
+        } else {
+          kop[kt][s] = *reinterpret_cast<const bf16x8_t*>(p.k_cache + (e + 32 * s + 8 * g) * esz);
+        }
+      }
+    }
+    // ---- V rows (coalesced) into the wave's LDS stage
+    if (FP8) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = 8 * i + (lane >> 3);
+        int key = kb + r;
+        key = key < L ? key : L - 1;
+        const int64_t e = blk_base + static_cast<int64_t>(off0 + key - kb) * p.tok_stride + (lane & 7) * 16;
+        const uint4 w = *reinterpret_cast<const uint4*>(p.v_cache + e);
+        const bf16x8_t a = fp8x8_to_bf16(make_uint2(w.x, w.y));
+        const bf16x8_t b = fp8x8_to_bf16(make_uint2(w.z, w.w));
+        uint32_t* dst = vst + r * kVPitch + (lane & 7) * 8;
+        *reinterpret_cast<bf16x8_t*>(dst) = a;
+        *reinterpret_cast<bf16x8_t*>(dst + 4) = b;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int r = 4 * i + g;
+        int key = kb + r;
+        key = key < L ? key : L - 1;
+        const int64_t e = blk_base + static_cast<int64_t>(off0 + key - kb) * p.tok_stride + m16 * 8;
+        const uint4 w = *reinterpret_cast<const uint4*>(p.v_cache + e * 2);
+        *reinterpret_cast<uint4*>(vst + r * kVPitch + m16 * 4) = w;
+      }
+    }
+
+    // ---- S^T = K . Q^T
+    f32x4_t sacc[2][NT];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        f32x4_t a = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) a = mfma(kop[kt][s], qop[nt][s], a);
+        sacc[kt][nt] = a;
+      }
+    }
+
+    // ---- online softmax (per query column; lanes l, l^16, l^32, l^48 share one)
+    bf16x8_t pb[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      float sv[8];
+      float cmax = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int key = kb + kt * 16 + 4 * g + i;
+          float v = sacc[kt][nt][i] * sl2;
+          v = key <= lim[nt] ? v : -INFINITY;
+          sv[kt * 4 + i] = v;
+          cmax = fmaxf(cmax, v);
+        }
+      }
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 16, kWave));
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 32, kWave));
+      const float m_new = fmaxf(m_run[nt], cmax);
+      const float msub = m_new == -INFINITY ? 0.0f : m_new;
+      const float alpha = exp2f_fast(m_run[nt] - msub);
+      float psum = 0.0f;
+      float pv[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        pv[k] = exp2f_fast(sv[k] - msub);
+        psum += pv[k];
+      }
+      l_run[nt] = l_run[nt] * alpha + psum;
+      m_run[nt] = m_new;
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[nt][t][i] *= alpha;
+      }
+      uint4 pk = make_uint4(pack_bf16(pv[0], pv[1]), pack_bf16(pv[2], pv[3]),
+                            pack_bf16(pv[4], pv[5]), pack_bf16(pv[6], pv[7]));
+      pb[nt] = __builtin_bit_cast(bf16x8_t, pk);
+    }
+
+    // make this wave's LDS writes visible to its own lanes before the reads
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+
+    // ---- O^T += V^T . P^T ; pair pp covers d = 32*pp + 2*m + {0 (even tile), 1 (odd tile)}
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) {
+      uint32_t w[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int key = (j < 4) ? (4 * g + j) : (16 + 4 * g + (j - 4));
+        w[j] = vst[key * kVPitch + 16 * pp + m16];
+      }
+      uint4 ev, od;
+      ev.x = __builtin_amdgcn_perm(w[1], w[0], 0x05040100u);
+      ev.y = __builtin_amdgcn_perm(w[3], w[2], 0x05040100u);
+      ev.z = __builtin_amdgcn_perm(w[5], w[4], 0x05040100u);
+      ev.w = __builtin_amdgcn_perm(w[7], w[6], 0x05040100u);
+      od.x = __builtin_amdgcn_perm(w[1], w[0], 0x07060302u);
+      od.y = __builtin_amdgcn_perm(w[3], w[2], 0x07060302u);
+      od.z = __builtin_amdgcn_perm(w[5], w[4], 0x07060302u);
+      od.w = __builtin_amdgcn_perm(w[7], w[6], 0x07060302u);
+      const bf16x8_t ea = __builtin_bit_cast(bf16x8_t, ev);
+      const bf16x8_t oa = __builtin_bit_cast(bf16x8_t, od);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        acc[nt][2 * pp] = mfma(ea, pb[nt], acc[nt][2 * pp]);
+        acc[nt][2 * pp + 1] = mfma(oa, pb[nt], acc[nt][2 * pp + 1]);
+      }
+    }
+    // the next iteration overwrites the stage: finish these reads first
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  }
+
+  // ---- merge the four waves
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    l_run[nt] += __shfl_xor(l_run[nt], 16, kWave);
+    l_run[nt] += __shfl_xor(l_run[nt], 32, kWave);
+  }
+  float* sm_m = reinterpret_cast<float*>(lds + kWaves * kVStage);
+  float* sm_l = sm_m + kWaves * 64;
+  float* sacc_lds = reinterpret_cast<float*>(lds);   // [wave][16 cols][kAccPitch]
+  __syncthreads();
+  if (g == 0) {
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      sm_m[wave * 64 + nt * 16 + m16] = m_run[nt];
+      sm_l[wave * 64 + nt * 16 + m16] = l_run[nt];
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int col = nt * 16 + m16;
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w * 64 + col]);
+    const float f = (m_run[nt] == -INFINITY) ? 0.0f : exp2f_fast(m_run[nt] - M);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[nt][t][i] *= f;
+    }
+  }
+
+  const int ccol = threadIdx.x >> 4;          // 0..15: column within the N tile
+  const int dgrp = threadIdx.x & 15;          // 8 consecutive d per thread
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    // scatter this wave's O^T tile as [col][d] floats
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) {
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d = 32 * pp + 2 * (4 * g + i) + e;
+          sacc_lds[(wave * 16 + m16) * kAccPitch + d] = acc[nt][2 * pp + e][i];
+        }
+      }
+    }
+    __syncthreads();
+    const int n = nt * 16 + ccol;
+    if (n < rows) {
+      float M = -INFINITY;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w * 64 + n]);
+      float ltot = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const float mw = sm_m[w * 64 + n];
+        ltot += (mw == -INFINITY) ? 0.0f : sm_l[w * 64 + n] * exp2f_fast(mw - M);
+      }
+      float o[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        float s = 0.0f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) s += sacc_lds[(w * 16 + ccol) * kAccPitch + dgrp * 8 + k];
+        o[k] = ltot > 0.0f ? s / ltot * vscale : 0.0f;
+      }
+      const int j = n / p.group, hh = n % p.group;
+      const int t = q_start + j;
+      const int h = kvh * p.group + hh;
+      if (nsplit == 1) {
+        uint16_t* op = p.out + static_cast<int64_t>(t) * p.out_row_stride +
+                       static_cast<int64_t>(h) * p.out_head_stride + dgrp * 8;
+        *reinterpret_cast<uint4*>(op) = make_uint4(pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]),
+                                                   pack_bf16(o[4], o[5]), pack_bf16(o[6], o[7]));
+      } else {
+        const int64_t slot = (static_cast<int64_t>(t) * p.hq + h) * p.max_splits + split;
+        float* wo = p.ws_o + slot * kD + dgrp * 8;
+        *reinterpret_cast<float4*>(wo) = make_float4(o[0], o[1], o[2], o[3]);
+        *reinterpret_cast<float4*>(wo + 4) = make_float4(o[4], o[5], o[6], o[7]);
+        if (dgrp == 0) p.ws_lse[slot] = ltot > 0.0f ? M + __log2f(ltot) : -INFINITY;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// Merge split partials: one wave per (token row, q head); lane covers 2 d.
+__global__ void __launch_bounds__(kThreads)
+combine_kernel(AttnParams p) {
+  const int t = blockIdx.x;
+  const int h = blockIdx.y * kWaves + threadIdx.x / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  if (h >= p.hq || t >= p.num_tokens) return;
+  int seq;
+  if (p.cu_q) {
+    if (t < p.cu_q[0] || t >= p.cu_q[p.num_seqs]) return;
+    int lo = 0, hi = p.num_seqs;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (p.cu_q[mid] <= t) lo = mid; else hi = mid;
+    }
+    seq = lo;
+  } else {
+    seq = t;
+  }
+  int q_start, q_len, L;
+  seq_geometry(p, seq, q_start, q_len, L);
+  if (t - q_start >= q_len) return;
+  const int nsplit = (L + p.split_len - 1) / p.split_len;
+  if (nsplit <= 1) return;
+  const int64_t base = (static_cast<int64_t>(t) * p.hq + h) * p.max_splits;
+  float M = -INFINITY;
+  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, p.ws_lse[base + s]);
+  float wsum = 0.0f, o0 = 0.0f, o1 = 0.0f;
+  for (int s = 0; s < nsplit; ++s) {
+    const float lse = p.ws_lse[base + s];
+    const float w = (lse == -INFINITY) ? 0.0f : exp2f_fast(lse - M);
+    const float2 v = *reinterpret_cast<const float2*>(p.ws_o + (base + s) * kD + 2 * lane);
+    wsum += w;
+    o0 += w * v.x;
+    o1 += w * v.y;
+  }
+  const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
+  uint16_t* op = p.out + static_cast<int64_t>(t) * p.out_row_stride +
+                 static_cast<int64_t>(h) * p.out_head_stride + 2 * lane;
+  *reinterpret_cast<uint32_t*>(op) = pack_bf16(o0 * inv, o1 * inv);
+}
+
+void choose_split(int32_t num_seqs, int32_t num_kv_heads, int32_t max_k, int32_t* split_len,
+                  int32_t* max_splits) {
+  const int64_t base = static_cast<int64_t>(num_seqs > 0 ? num_seqs : 1) * (num_kv_heads > 0 ? num_kv_heads : 1);
+  int64_t want = (kTargetWorkgroups + base - 1) / base;
+  const int32_t mk = max_k > 1 ? max_k : 1;
+  int64_t by_len = (mk + kMinSplit - 1) / kMinSplit;
+  int64_t s = want < by_len ? want : by_len;
+  if (s < 1) s = 1;
+  int32_t len = static_cast<int32_t>((mk + s - 1) / s);
+  len = (len + kMinSplit - 1) / kMinSplit * kMinSplit;
+  *split_len = len;
+  *max_splits = (mk + len - 1) / len;
+}
+
+size_t workspace_bytes(int32_t num_seqs, int32_t num_tokens, int32_t hq, int32_t hkv, int32_t max_k) {
+  int32_t len, ms;
+  choose_split(num_seqs, hkv, max_k, &len, &ms);
+  if (ms <= 1) return 0;
+  const size_t slots = static_cast<size_t>(num_tokens) * hq * ms;
+  return slots * kD * sizeof(float) + slots * sizeof(float) + 256;
+}
+
+template <int NT>
+void launch_nt(const AttnParams& p, bool fp8, dim3 grid, hipStream_t s) {
+  if (fp8)
+    paged_attention_kernel<NT, true><<<grid, kThreads, 0, s>>>(p);
+  else
+    paged_attention_kernel<NT, false><<<grid, kThreads, 0, s>>>(p);
+}
+
+int run_attention(AttnParams& p, int kv_dtype, void* workspace, size_t workspace_bytes_, hipStream_t s) {
+  if (p.hq <= 0 || p.hkv <= 0 || p.hq % p.hkv != 0) return NVA_ERR_ARG;
+  if (kv_dtype != NVA_KV_BF16 && kv_dtype != NVA_KV_FP8_E4M3) return NVA_ERR_ARG;
+  if (p.num_seqs < 0 || p.num_tokens < 0 || p.max_q < 0 || p.max_k < 0) return NVA_ERR_ARG;
+  if (p.num_seqs == 0 || p.num_tokens == 0 || p.max_q == 0) return NVA_OK;
+  if (!p.q || !p.k_cache || !p.v_cache || !p.block_tables || !p.out) return NVA_ERR_ARG;
+  if (p.block_size <= 0 || p.block_size % kChunk != 0 || p.num_blocks <= 0) return NVA_ERR_UNSUPPORTED;
+  if (p.bt_cols < 0 || p.bt_stride < p.bt_cols) return NVA_ERR_ARG;
+  p.group = p.hq / p.hkv;
+  const int tile_rows = p.max_q * p.group;
+  if (tile_rows > 64) return NVA_ERR_UNSUPPORTED;
+  // alignment of 16-byte vector accesses
+  const int64_t vec_elems = kv_dtype == NVA_KV_BF16 ? 8 : 16;
+  if (!aligned16(p.q) || !aligned16(p.out) || !aligned16(p.k_cache) || !aligned16(p.v_cache) ||
+      p.q_row_stride % 8 || p.q_head_stride % 8 || p.out_row_stride % 8 || p.out_head_stride % 8 ||
+      p.blk_stride % vec_elems || p.tok_stride % vec_elems || p.head_stride % vec_elems)
+    return NVA_ERR_UNSUPPORTED;
+  choose_split(p.num_seqs, p.hkv, p.max_k, &p.split_len, &p.max_splits);
+  if (p.max_splits > 1) {
+    const size_t need = workspace_bytes(p.num_seqs, p.num_tokens, p.hq, p.hkv, p.max_k);
+    if (!workspace || workspace_bytes_ < need || !aligned16(workspace)) return NVA_ERR_WORKSPACE;
+    const size_t slots = static_cast<size_t>(p.num_tokens) * p.hq * p.max_splits;
+    p.ws_o = static_cast<float*>(workspace);
+    p.ws_lse = p.ws_o + slots * kD;
+  } else {
+    p.ws_o = nullptr;
+    p.ws_lse = nullptr;
+  }
+  const bool fp8 = kv_dtype == NVA_KV_FP8_E4M3;
+  dim3 grid(p.max_splits, p.hkv, p.num_seqs);
+  const int nt = (tile_rows + 15) / 16;
+  if (nt <= 1)
+    launch_nt<1>(p, fp8, grid, s);
+  else if (nt == 2)
+    launch_nt<2>(p, fp8, grid, s);
+  else
+    launch_nt<4>(p, fp8, grid, s);
+  if (hipGetLastError() != hipSuccess) return NVA_ERR_LAUNCH;
+  if (p.max_splits > 1) {
+    dim3 cgrid(p.num_tokens, (p.hq + kWaves - 1) / kWaves);
+    combine_kernel<<<cgrid, kThreads, 0, s>>>(p);
+  }
+  return launch_status();
+}
+
+}  // namespace
+}  // namespace nva
+
+using namespace nva;
+
+extern "C" size_t nva_paged_attention_workspace_size(int32_t num_seqs, int32_t num_tokens,
+                                                     int32_t num_q_heads, int32_t num_kv_heads,
+                                                     int32_t head_dim, int32_t max_seqlen_k) {
+  if (num_seqs <= 0 || num_tokens <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim != kD)
+    return 0;
+  return workspace_bytes(num_seqs, num_tokens, num_q_heads, num_kv_heads, max_seqlen_k);
+}
+
+extern "C" int nva_paged_attention_varlen(
+    const void* q, int64_t q_row_stride, int64_t q_head_stride, const void* k_cache,
+    const void* v_cache, int kv_dtype, int64_t cache_block_stride, int64_t cache_token_stride,
+    int64_t cache_head_stride, int32_t num_blocks, int32_t block_size,
+    const int32_t* cu_seqlens_q, const int32_t* cu_seqlens_k, const int32_t* block_tables,
+    int64_t block_table_stride, int32_t max_blocks_per_seq, int32_t num_seqs, int32_t num_tokens, int32_t max_seqlen_q,
+    int32_t max_seqlen_k, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+    float softmax_scale, const float* k_scale, const float* v_scale, void* out,
+    int64_t out_row_stride, int64_t out_head_stride, void* workspace, size_t workspace_bytes_,
+    void* stream) {
+  if (head_dim != kD) return NVA_ERR_UNSUPPORTED;
+  if (!cu_seqlens_q || !cu_seqlens_k) return NVA_ERR_ARG;
+  AttnParams p = {};
+  p.q = static_cast<const uint16_t*>(q);
+  p.q_row_stride = q_row_stride;
+  p.q_head_stride = q_head_stride;
+  p.k_cache = static_cast<const uint8_t*>(k_cache);
+  p.v_cache = static_cast<const uint8_t*>(v_cache);
+  p.blk_stride = cache_block_stride;
+  p.tok_stride = cache_token_stride;
+  p.head_stride = cache_head_stride;
+  p.num_blocks = num_blocks;
+  p.block_size = block_size;
+  p.cu_q = cu_seqlens_q;
+  p.cu_k = cu_seqlens_k;
+  p.seqlens = nullptr;
+  p.block_tables = block_tables;
+  p.bt_stride = block_table_stride;
+  p.bt_cols = max_blocks_per_seq;
+  p.num_seqs = num_seqs;
+  p.num_tokens = num_tokens;
+  p.max_q = max_seqlen_q;
+  p.max_k = max_seqlen_k;
+  p.hq = num_q_heads;
+  p.hkv = num_kv_heads;
+  p.scale_log2 = softmax_scale * kLog2e;
+  p.k_scale = k_scale;
+  p.v_scale = v_scale;
+  p.out = static_cast<uint16_t*>(out);
+  p.out_row_stride = out_row_stride;
+  p.out_head_stride = out_head_stride;
+  return run_attention(p, kv_dtype, workspace, workspace_bytes_, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int nva_paged_attention_decode(
+    const void* q, int64_t q_row_stride, int64_t q_head_stride, const void* k_cache,
+    const void* v_cache, int kv_dtype, int64_t cache_block_stride, int64_t cache_token_stride,
+    int64_t cache_head_stride, int32_t num_blocks, int32_t block_size,
+    const int32_t* cache_seqlens, const int32_t* block_tables, int64_t block_table_stride,
+    int32_t max_blocks_per_seq, int32_t num_seqs, int32_t max_seqlen_k, int32_t num_q_heads, int32_t num_kv_heads,
+    int32_t head_dim, float softmax_scale, const float* k_scale, const float* v_scale, void* out,
+    int64_t out_row_stride, int64_t out_head_stride, void* workspace, size_t workspace_bytes_,
+    void* stream) {
+  if (head_dim != kD) return NVA_ERR_UNSUPPORTED;
+  if (!cache_seqlens) return NVA_ERR_ARG;
+  AttnParams p = {};
+  p.q = static_cast<const uint16_t*>(q);
+  p.q_row_stride = q_row_stride;
+  p.q_head_stride = q_head_stride;
+  p.k_cache = static_cast<const uint8_t*>(k_cache);
+  p.v_cache = static_cast<const uint8_t*>(v_cache);
+  p.blk_stride = cache_block_stride;
+  p.tok_stride = cache_token_stride;
+  p.head_stride = cache_head_stride;
+  p.num_blocks = num_blocks;
+  p.block_size = block_size;
+  p.cu_q = nullptr;
+  p.cu_k = nullptr;
+  p.seqlens = cache_seqlens;
+  p.block_tables = block_tables;
+  p.bt_stride = block_table_stride;
+  p.bt_cols = max_blocks_per_seq;
+  p.num_seqs = num_seqs;
+  p.num_tokens = num_seqs;
+  p.max_q = 1;
+  p.max_k = max_seqlen_k;
+  p.hq = num_q_heads;
+  p.hkv = num_kv_heads;
+  p.scale_log2 = softmax_scale * kLog2e;
+  p.k_scale = k_scale;
+  p.v_scale = v_scale;
+  p.out = static_cast<uint16_t*>(out);
+  p.out_row_stride = out_row_stride;
+  p.out_head_stride = out_head_stride;
+  return run_attention(p, kv_dtype, workspace, workspace_bytes_, static_cast<hipStream_t>(stream));
+}

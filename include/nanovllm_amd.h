@@ -1,0 +1,229 @@
+/*
+ * nanovllm_amd.h -- C ABI of the MI355X (gfx950) EAGLE3 speculative-step
+ * kernels.  Built into libnanovllm_amd.so from extend-nano-vllm_amd/csrc/.
+ *
+ * Reference: kagami4243/extend-nano-vLLM (package `nanovllm`).  Each entry
+ * point names the reference call it replaces (file:line).  The reference's
+ * kernels are Python-callable Triton / FlashAttention-2 functions taking torch
+ * tensors; here the same operations take raw device pointers, element strides
+ * and sizes.
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers unless stated otherwise.  The caller owns
+ *     every buffer; nothing is allocated or freed inside the library.
+ *   - Strides are in ELEMENTS of the pointed-to type.
+ *   - `stream` is a hipStream_t (passed as void*); work is enqueued on it with
+ *     no host synchronisation, so every call may be captured in a HIP graph.
+ *   - bf16 tensors are passed as their 16-bit storage; KV caches are bf16
+ *     (NVA_KV_BF16) or OCP float8_e4m3fn (NVA_KV_FP8_E4M3).
+ *   - The return value is an nva_status; argument errors are detected on the
+ *     host before anything is launched.  Device-resident metadata (slots,
+ *     block ids, lengths) is bounds-checked inside the kernels: an
+ *     out-of-range slot or block id is skipped, never dereferenced.
+ *   - Calls on one stream are ordered; calls that share a workspace must not
+ *     run concurrently on different streams.
+ */
+#ifndef NANOVLLM_AMD_H
+#define NANOVLLM_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum nva_status {
+  NVA_OK = 0,
+  NVA_ERR_ARG = 1,          /* null pointer, bad size/stride/shape */
+  NVA_ERR_WORKSPACE = 2,    /* workspace missing or smaller than required */
+  NVA_ERR_UNSUPPORTED = 3,  /* valid but unsupported (e.g. head_dim != 128) */
+  NVA_ERR_LAUNCH = 4        /* the HIP runtime rejected a launch */
+};
+
+enum nva_kv_dtype { NVA_KV_BF16 = 0, NVA_KV_FP8_E4M3 = 1 };
+
+/* Human-readable name of a status code (static string). */
+const char *nva_status_string(int status);
+
+/* Library version string (static). */
+const char *nva_version(void);
+
+/* ---------------------------------------------------------------------
+ * K2a  KV-cache slot write.
+ * Replaces store_kvcache / store_kvcache_kernel
+ *   (nanovllm/layers/attention.py:189-217, kernel :14-43).
+ * key/value: bf16 [num_tokens, num_kv_heads, head_dim], head stride ==
+ *   head_dim, row strides key_row_stride / value_row_stride (views into a
+ *   fused QKV output are allowed).
+ * k_cache/v_cache: [num_slots, num_kv_heads * head_dim] contiguous (the
+ *   reference's [num_blocks, block_size, Hkv, D] layer view flattened),
+ *   slot = block_id * block_size + offset.
+ * Token t is written to slot_mapping[t]; negative slots (the reference's -1)
+ *   and slots >= num_slots are skipped.
+ * FP8: each element is stored as e4m3(x / scale), round-to-nearest-even,
+ *   saturating to +-448; k_scale / v_scale are device fp32 scalars (NULL =
+ *   1.0).  bf16 caches ignore the scales, as the reference does.
+ * ------------------------------------------------------------------- */
+int nva_store_kvcache(const void *key, int64_t key_row_stride,
+                      const void *value, int64_t value_row_stride,
+                      void *k_cache, void *v_cache, int kv_dtype,
+                      const int32_t *slot_mapping, int32_t num_tokens,
+                      int32_t num_kv_heads, int32_t head_dim, int64_t num_slots,
+                      const float *k_scale, const float *v_scale, void *stream);
+
+/* ---------------------------------------------------------------------
+ * K2b  Rollback of rejected draft rows.
+ * Device mirror of the reference's logical rollback after greedy
+ *   verification: Sequence.truncate_tokens + BlockManager.truncate
+ *   (nanovllm/engine/scheduler.py:165-170, block_manager.py:197-205,
+ *   sequence.py:84-91).  Rows j > accept_len[i] of sequence i (verify rows
+ *   [cu_seqlens_q[i], cu_seqlens_q[i+1])) are rejected: their slot_mapping
+ *   entry becomes -1 and seqlens_k[i] drops by the number of rejected rows,
+ *   so later attention never reads them.  accept_len is clamped to
+ *   [0, q_i - 1].
+ * With poison != 0 the rejected slots are zeroed in num_layers layers of the
+ *   caches (k_cache / v_cache point at layer 0; layer l is at
+ *   + l * layer_stride elements; each slot row has row_elems elements).
+ *   With poison == 0 the caches may be NULL.
+ * ------------------------------------------------------------------- */
+int nva_rollback(const int32_t *cu_seqlens_q, const int32_t *accept_len, int32_t num_seqs,
+                 int32_t *slot_mapping, int32_t *seqlens_k,
+                 void *k_cache, void *v_cache, int kv_dtype, int32_t num_layers,
+                 int64_t layer_stride, int32_t row_elems, int64_t num_slots, int poison,
+                 void *stream);
+
+/* ---------------------------------------------------------------------
+ * K3  EAGLE3 auxiliary hidden-state add + concat + row gather.
+ * Replaces `hidden_states + residual` at the aux layers, torch.cat(aux, -1)
+ *   (nanovllm/models/qwen3.py:284-289) and the per-sequence row slicing that
+ *   feeds the draft fc (nanovllm/engine/model_runner.py:1073, :1236-1242;
+ *   nanovllm/engine/llm_engine.py:170).
+ * hidden / residual: HOST arrays of num_layers (1..4) device pointers, each a
+ *   bf16 [rows, hidden_size] matrix with row stride in_row_stride.
+ * out[r, l*hidden_size + c] = bf16(f32(hidden[l][src_rows[r], c]) +
+ *                                 f32(residual[l][src_rows[r], c]))
+ *   rounded to nearest even; out has row stride out_row_stride.
+ * src_rows entries outside [0, num_in_rows) produce zero rows.
+ * ------------------------------------------------------------------- */
+int nva_aux_gather(const void *const *hidden, const void *const *residual, int32_t num_layers,
+                   int64_t in_row_stride, int32_t hidden_size, int32_t num_in_rows,
+                   const int32_t *src_rows, int32_t num_rows,
+                   void *out, int64_t out_row_stride, void *stream);
+
+/* ---------------------------------------------------------------------
+ * K4a  Vocab argmax fused with the greedy accepted-prefix / bonus scan.
+ * Replaces the per-sequence `target_logits[start:end].argmax(dim=-1).tolist()`
+ *   of verify_eagle3_batch (nanovllm/engine/model_runner.py:1066-1074) and
+ *   verify_greedy_proposals (nanovllm/engine/speculative.py:11-30).
+ * logits: bf16 [num_tokens, vocab], row stride row_stride.
+ * cu_seqlens_q: [num_seqs + 1] verify row offsets (device).
+ * input_ids: the verify input tokens [num_tokens] (int64, device): proposal j
+ *   of sequence i is input_ids[cu_seqlens_q[i] + 1 + j], j < q_i - 1 (row 0
+ *   of each sequence is the previous target token).
+ * Outputs: argmax[num_tokens] (torch.argmax semantics on bf16: first index of
+ *   the maximum, NaN is the maximum, -0 == +0); accept_len[num_seqs] = first
+ *   j with proposal_j != argmax[row j], else q_i - 1; bonus[num_seqs] =
+ *   argmax[row accept_len] (the replacement or bonus token).  A sequence with
+ *   q_i == 0 gets accept_len 0 and bonus -1.
+ * workspace: nva_argmax_workspace_size(num_tokens, num_seqs, vocab) bytes,
+ *   ZERO-FILLED by the caller before its first use; every call leaves it
+ *   zero-filled again (its counters reset themselves).
+ * ------------------------------------------------------------------- */
+size_t nva_argmax_workspace_size(int32_t num_rows, int32_t num_seqs, int32_t vocab);
+
+int nva_argmax_accept(const void *logits, int64_t row_stride, int32_t vocab,
+                      const int32_t *cu_seqlens_q, int32_t num_seqs, int32_t num_tokens,
+                      const int64_t *input_ids,
+                      int32_t *argmax, int32_t *accept_len, int32_t *bonus,
+                      void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------------
+ * K4b  Row argmax with an optional index map (greedy sampling).
+ * Replaces Eagle3ForCausalLM.sample_greedy's argmax + d2t lookup
+ *   (nanovllm/models/eagle3.py:294-296) and the greedy branch of Sampler
+ *   (nanovllm/layers/sampler.py:10-19, temperature 0).
+ * out[r] = idx + (index_map ? index_map[idx] : 0), idx = argmax of row r
+ *   (same semantics as nva_argmax_accept); out is int64 [num_rows].
+ * workspace: as for nva_argmax_accept (num_seqs = 0).
+ * ------------------------------------------------------------------- */
+int nva_argmax_rows(const void *logits, int64_t row_stride, int32_t vocab, int32_t num_rows,
+                    const int64_t *index_map, int64_t *out,
+                    void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------------
+ * K1  Paged verify attention.
+ *
+ * Shared arguments:
+ *   q: bf16 [rows, num_q_heads, head_dim] with strides q_row_stride,
+ *      q_head_stride (d contiguous).  out: bf16, same shape, strides
+ *      out_row_stride, out_head_stride.
+ *   k_cache / v_cache: one layer, [num_blocks, block_size, num_kv_heads,
+ *      head_dim] addressed by cache_block_stride / cache_token_stride /
+ *      cache_head_stride (d contiguous), kv_dtype bf16 or fp8 e4m3.
+ *   block_tables: int32 [num_seqs, max_blocks_per_seq], row stride
+ *      block_table_stride; key n of sequence i is at block
+ *      block_tables[i][n / block_size], offset n % block_size.  Keys beyond
+ *      max_blocks_per_seq * block_size and block ids outside [0, num_blocks)
+ *      are treated as empty (masked), never dereferenced.
+ *   Query rows at or beyond num_tokens (from inconsistent cu_seqlens_q) are
+ *      skipped.
+ *   softmax_scale multiplies q.k; for FP8 caches the scores are also
+ *      multiplied by *k_scale and the output by *v_scale (NULL = 1.0), as in
+ *      the reference's FP8 decode kernel; bf16 caches ignore the scales.
+ *   GQA: query head h reads kv head h / (num_q_heads / num_kv_heads).
+ *   head_dim must be 128 and block_size a multiple of 32;
+ *      max_seqlen_q * (num_q_heads / num_kv_heads) must be <= 64.
+ *   workspace: nva_paged_attention_workspace_size(...) bytes (split-KV
+ *      partial results; needs no initialisation).
+ * ------------------------------------------------------------------- */
+
+/* Replaces flash_attn_varlen_func(q, k_cache, v_cache, max_seqlen_q,
+ *   cu_seqlens_q, max_seqlen_k, cu_seqlens_k, softmax_scale, causal=True,
+ *   block_table) -- the EAGLE3 verify attention (nanovllm/layers/
+ *   attention.py:385-395).  Sequence i has q_i = cu_seqlens_q[i+1] -
+ *   cu_seqlens_q[i] query rows and L_i = cu_seqlens_k[i+1] - cu_seqlens_k[i]
+ *   keys including its new rows; causality is bottom-right aligned: query row
+ *   j sees keys [0, L_i - q_i + j].  max_seqlen_q / max_seqlen_k bound q_i and
+ *   L_i (they size the grid; larger device values are clipped to them). */
+size_t nva_paged_attention_workspace_size(int32_t num_seqs, int32_t num_tokens,
+                                          int32_t num_q_heads, int32_t num_kv_heads,
+                                          int32_t head_dim, int32_t max_seqlen_k);
+
+int nva_paged_attention_varlen(const void *q, int64_t q_row_stride, int64_t q_head_stride,
+                               const void *k_cache, const void *v_cache, int kv_dtype,
+                               int64_t cache_block_stride, int64_t cache_token_stride,
+                               int64_t cache_head_stride, int32_t num_blocks, int32_t block_size,
+                               const int32_t *cu_seqlens_q, const int32_t *cu_seqlens_k,
+                               const int32_t *block_tables, int64_t block_table_stride,
+                               int32_t max_blocks_per_seq, int32_t num_seqs, int32_t num_tokens,
+                               int32_t max_seqlen_q, int32_t max_seqlen_k,
+                               int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                               float softmax_scale, const float *k_scale, const float *v_scale,
+                               void *out, int64_t out_row_stride, int64_t out_head_stride,
+                               void *workspace, size_t workspace_bytes, void *stream);
+
+/* Replaces flash_attn_with_kvcache(q[:, None], k_cache, v_cache,
+ *   cache_seqlens, block_table, softmax_scale, causal=True) -- the one-query
+ *   decode used by the draft (nanovllm/layers/attention.py:396-399) -- and
+ *   fp8_paged_decode_attention(q, k_cache, v_cache, context_lens,
+ *   block_tables, scale, k_scale, v_scale) (nanovllm/layers/
+ *   attention.py:249-293).  Row r (of num_seqs) is one query that sees keys
+ *   [0, cache_seqlens[r]) through block_tables row r. */
+int nva_paged_attention_decode(const void *q, int64_t q_row_stride, int64_t q_head_stride,
+                               const void *k_cache, const void *v_cache, int kv_dtype,
+                               int64_t cache_block_stride, int64_t cache_token_stride,
+                               int64_t cache_head_stride, int32_t num_blocks, int32_t block_size,
+                               const int32_t *cache_seqlens,
+                               const int32_t *block_tables, int64_t block_table_stride,
+                               int32_t max_blocks_per_seq, int32_t num_seqs, int32_t max_seqlen_k,
+                               int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                               float softmax_scale, const float *k_scale, const float *v_scale,
+                               void *out, int64_t out_row_stride, int64_t out_head_stride,
+                               void *workspace, size_t workspace_bytes, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NANOVLLM_AMD_H */

@@ -1,0 +1,88 @@
+"""Input generators shared by the tests (seeded, generated on the CPU so the
+GPU kernels and the CPU oracle consume byte-identical data)."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+
+def bits(t: torch.Tensor) -> np.ndarray:
+    """Storage bits of a CPU bf16 / fp8 tensor as a numpy array."""
+    t = t.detach().cpu().contiguous()
+    if t.dtype == torch.bfloat16:
+        return t.view(torch.int16).numpy().view(np.uint16)
+    if t.dtype == torch.float8_e4m3fn:
+        return t.view(torch.uint8).numpy()
+    raise TypeError(t.dtype)
+
+
+def from_bits(a: np.ndarray, dtype: torch.dtype) -> torch.Tensor:
+    if dtype == torch.bfloat16:
+        return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16)
+    if dtype == torch.float8_e4m3fn:
+        return torch.from_numpy(np.ascontiguousarray(a).view(np.uint8)).view(torch.float8_e4m3fn)
+    raise TypeError(dtype)
+
+
+def acceptance_logits(batch: int, k: int, vocab: int, p_accept: float, seed: int):
+    """Config-1 style verify batch: bf16 logits [B*(k+1), V] ~ N(0,1); for
+    each (sequence, draft position j < k), with probability p_accept the
+    draft token's logit is raised to the row max + 1.0 (in fp32, then cast).
+
+    Returns (logits bf16 CPU, cu_q int32, input_ids int64, proposals [B, k])."""
+    g = torch.Generator().manual_seed(seed)
+    logits = torch.randn(batch, k + 1, vocab, generator=g)
+    proposals = torch.randint(0, vocab, (batch, k), generator=g)
+    raise_mask = torch.rand(batch, k, generator=g) < p_accept
+    for s in range(batch):
+        for j in range(k):
+            if raise_mask[s, j]:
+                row = logits[s, j]
+                row[proposals[s, j]] = row.max() + 1.0
+    logits = logits.to(torch.bfloat16).reshape(batch * (k + 1), vocab)
+    cu_q = torch.arange(0, batch * (k + 1) + 1, k + 1, dtype=torch.int32)
+    input_ids = torch.zeros(batch, k + 1, dtype=torch.int64)
+    input_ids[:, 0] = torch.randint(0, vocab, (batch,), generator=g)
+    input_ids[:, 1:] = proposals
+    return logits, cu_q, input_ids.reshape(-1), proposals
+
+
+def paged_case(seed: int, batch: int, q_len, ctx_lo: int, ctx_hi: int, hq: int, hkv: int,
+               head_dim: int = 128, block_size: int = 256, spare_blocks: int = 3,
+               scale: float = 0.5):
+    """A shuffled paged KV layout plus new rows to verify.
+
+    q_len: int or list per sequence.  Context lengths L_i ~ U[ctx_lo, ctx_hi]
+    include the q_i new rows.  Returns a dict of CPU tensors: q [T,Hq,D],
+    k_new/v_new [T,Hkv,D], k_cache/v_cache [NB,bs,Hkv,D] (random old
+    content), block_tables [B, max_blocks] (-1 padded), cu_q, cu_k, lens,
+    slot_mapping [T]."""
+    g = torch.Generator().manual_seed(seed)
+    qs = [q_len] * batch if isinstance(q_len, int) else list(q_len)
+    lens = torch.randint(ctx_lo, ctx_hi + 1, (batch,), generator=g).tolist()
+    lens = [max(L, q) for L, q in zip(lens, qs)]
+    nblk = [(L + block_size - 1) // block_size for L in lens]
+    total = sum(nblk) + spare_blocks
+    perm = torch.randperm(total, generator=g).tolist()
+    max_blocks = max(nblk) + 1
+    bt = torch.full((batch, max_blocks), -1, dtype=torch.int32)
+    pos = 0
+    for i, n in enumerate(nblk):
+        bt[i, :n] = torch.tensor(perm[pos:pos + n], dtype=torch.int32)
+        pos += n
+    t = sum(qs)
+    k_cache = (torch.randn(total, block_size, hkv, head_dim, generator=g) * scale).to(torch.bfloat16)
+    v_cache = (torch.randn(total, block_size, hkv, head_dim, generator=g) * scale).to(torch.bfloat16)
+    q = (torch.randn(t, hq, head_dim, generator=g) * scale).to(torch.bfloat16)
+    k_new = (torch.randn(t, hkv, head_dim, generator=g) * scale).to(torch.bfloat16)
+    v_new = (torch.randn(t, hkv, head_dim, generator=g) * scale).to(torch.bfloat16)
+    cu_q = torch.tensor([0] + np.cumsum(qs).tolist(), dtype=torch.int32)
+    cu_k = torch.tensor([0] + np.cumsum(lens).tolist(), dtype=torch.int32)
+    slots = []
+    for i, (L, qn) in enumerate(zip(lens, qs)):
+        for p in range(L - qn, L):
+            slots.append(int(bt[i, p // block_size]) * block_size + p % block_size)
+    return dict(q=q, k_new=k_new, v_new=v_new, k_cache=k_cache, v_cache=v_cache,
+                block_tables=bt, cu_q=cu_q, cu_k=cu_k, lens=torch.tensor(lens, dtype=torch.int32),
+                slot_mapping=torch.tensor(slots, dtype=torch.int32), q_lens=qs,
+                block_size=block_size)

@@ -1,0 +1,59 @@
+"""The C-ABI library loads (no GPU needed) and exports every entry point the
+header declares; the Python binding declares exactly those symbols."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from nanovllm_amd import _native
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "nanovllm_amd.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(nva_\w+)\s*\(", text)))
+
+
+def test_header_declares_the_hot_path_entry_points():
+    syms = declared_symbols()
+    for name in ("nva_store_kvcache", "nva_rollback", "nva_aux_gather", "nva_argmax_accept",
+                 "nva_argmax_rows", "nva_paged_attention_varlen", "nva_paged_attention_decode"):
+        assert name in syms
+
+
+def test_library_exports_every_declared_symbol():
+    if not os.path.exists(_native.LIB_PATH):
+        pytest.fail(f"{_native.LIB_PATH} missing: run __graft_entry__.build()")
+    lib = ctypes.CDLL(_native.LIB_PATH)
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, missing
+
+
+def test_binding_covers_the_header():
+    assert sorted(_native.SIGNATURES) == declared_symbols()
+
+
+def test_host_side_argument_errors_without_gpu():
+    lib = _native.load()
+    assert lib.nva_version().startswith(b"nanovllm_amd")
+    # bad arguments are rejected on the host before any launch
+    assert lib.nva_store_kvcache(None, 0, None, 0, None, None, 7, None, 4, 1, 128, 10,
+                                 None, None, None) == _native.NVA_ERR_ARG
+    assert lib.nva_aux_gather(None, None, 9, 0, 0, 0, None, 1, None, 0, None) == _native.NVA_ERR_ARG
+    assert lib.nva_paged_attention_decode(None, 0, 0, None, None, 0, 0, 0, 0, 1, 256, None, None,
+                                          0, 1, 1, 16, 8, 8, 64, 1.0, None, None, None, 0, 0,
+                                          None, 0, None) == _native.NVA_ERR_UNSUPPORTED
+    assert lib.nva_argmax_accept(None, 10, 5, None, 1, 1, None, None, None, None, None, 0,
+                                 None) == _native.NVA_ERR_ARG
+    # zero-size work is a no-op
+    assert lib.nva_argmax_rows(None, 8, 8, 0, None, None, None, 0, None) == _native.NVA_OK
+    assert lib.nva_argmax_workspace_size(384, 64, 151936) > 0
+    assert lib.nva_paged_attention_workspace_size(64, 384, 32, 8, 128, 2304) > 0
+    with pytest.raises(ValueError):
+        _native.check(_native.NVA_ERR_ARG, "probe")
+    with pytest.raises(_native.KernelError):
+        _native.check(_native.NVA_ERR_LAUNCH, "probe")

@@ -1,0 +1,372 @@
+"""GPU parity of the four hot-path kernels against the CPU oracle.
+
+Integer / byte work (argmax, accept, KV store, rollback, aux gather) must be
+bit-exact; attention must be within 2e-2 max-abs of the double-precision
+textbook result and FP8 decode within 2e-3 (the
+reference's own bound, tests/test_fp8_kv_cache.py:81 of the reference).
+Every call goes through the C ABI (nanovllm_amd.kernels -> libnanovllm_amd.so).
+"""
+import numpy as np
+import pytest
+import torch
+
+from helpers import acceptance_logits, bits, from_bits, paged_case
+from oracle import oracle
+
+pytestmark = pytest.mark.gpu
+
+ATTN_TOL = 2e-2
+FP8_TOL = 2e-3
+
+
+@pytest.fixture(scope="module")
+def K(cuda):
+    from nanovllm_amd import kernels
+
+    return kernels
+
+
+# ---------------------------------------------------------------- K4
+
+@pytest.mark.parametrize("batch,k,vocab,seed", [(8, 4, 151936, 0), (64, 5, 151936, 2),
+                                                 (3, 8, 1000, 5), (5, 1, 37, 6)])
+def test_argmax_accept_matches_oracle(K, cuda, batch, k, vocab, seed):
+    logits, cu_q, ids, _ = acceptance_logits(batch, k, vocab, 0.7, seed)
+    am, acc, bonus = K.argmax_accept(logits.to(cuda), cu_q.to(cuda), ids.to(cuda))
+    torch.cuda.synchronize()
+    ref_am = oracle.argmax_bf16(bits(logits))
+    ref_acc, ref_bonus = oracle.accept(cu_q.numpy(), ref_am, ids.numpy())
+    np.testing.assert_array_equal(am.cpu().numpy(), ref_am)
+    np.testing.assert_array_equal(acc.cpu().numpy(), ref_acc)
+    np.testing.assert_array_equal(bonus.cpu().numpy(), ref_bonus)
+    # and the torch reference semantics on the same bytes
+    np.testing.assert_array_equal(ref_am, logits.argmax(-1).numpy())
+
+
+def test_argmax_edge_values(K, cuda):
+    v = 70001
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(8, v, generator=g).to(torch.bfloat16)
+    xb = x.view(torch.int16)
+    x[0, 100] = 50.0
+    x[0, 60000] = 50.0                       # tie: first index wins
+    xb[1, 5000] = 0x7FC1                     # NaN beats everything
+    xb[1, 70000] = -64                       # 0xFFC0 negative NaN, later
+    x[2, :] = -1.0
+    x[2, 777] = -0.0
+    x[2, 778] = 0.0                          # -0 == +0 -> first
+    x[3, :] = float("-inf")                  # all -inf -> 0
+    x[4, :] = 3.0                            # all equal -> 0
+    x[5, v - 1] = 1e30                       # max at the last element (tail path)
+    x[6, 0] = float("inf")
+    xb[7, 69999] = 0x7F80                    # +inf late
+    x[7, 3] = 3e38
+    cu = torch.tensor([0, 3, 8], dtype=torch.int32)
+    ids = torch.zeros(8, dtype=torch.int64)
+    am, acc, bonus = K.argmax_accept(x.to(cuda), cu.to(cuda), ids.to(cuda))
+    ref = oracle.argmax_bf16(bits(x))
+    np.testing.assert_array_equal(ref, x.argmax(-1).numpy())
+    np.testing.assert_array_equal(am.cpu().numpy(), ref)
+    ra, rb = oracle.accept(cu.numpy(), ref, ids.numpy())
+    np.testing.assert_array_equal(acc.cpu().numpy(), ra)
+    np.testing.assert_array_equal(bonus.cpu().numpy(), rb)
+
+
+def test_argmax_accept_ragged_and_empty(K, cuda):
+    g = torch.Generator().manual_seed(3)
+    qs = [1, 9, 0, 4, 2, 0, 6]
+    t = sum(qs)
+    vocab = 5000
+    logits = torch.randn(t, vocab, generator=g).to(torch.bfloat16)
+    cu = torch.tensor([0] + np.cumsum(qs).tolist(), dtype=torch.int32)
+    ref_am = oracle.argmax_bf16(bits(logits))
+    ids = torch.randint(0, vocab, (t,), generator=g)
+    # make some proposals match so accept lengths vary
+    for i, q in enumerate(qs):
+        s = int(cu[i])
+        for j in range(q - 1):
+            if (i + j) % 3 != 2:
+                ids[s + 1 + j] = int(ref_am[s + j])
+    am, acc, bonus = K.argmax_accept(logits.to(cuda), cu.to(cuda), ids.to(cuda))
+    ra, rb = oracle.accept(cu.numpy(), ref_am, ids.numpy())
+    np.testing.assert_array_equal(acc.cpu().numpy(), ra)
+    np.testing.assert_array_equal(bonus.cpu().numpy(), rb)
+    assert rb[2] == -1 and ra[2] == 0
+
+
+def test_argmax_accept_graph_replay(K, cuda):
+    """Self-resetting counters: replaying a captured call stays correct."""
+    logits, cu_q, ids, _ = acceptance_logits(16, 5, 151936, 0.7, 9)
+    dl, dcu, dids = logits.to(cuda), cu_q.to(cuda), ids.to(cuda)
+    out = torch.empty(logits.shape[0] + 32, dtype=torch.int32, device=cuda)
+    K.argmax_accept(dl, dcu, dids, out=out)           # grows the workspace
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        K.argmax_accept(dl, dcu, dids, out=out)
+    for rep in range(4):
+        nl, ncu, nids, _ = acceptance_logits(16, 5, 151936, 0.5, 100 + rep)
+        dl.copy_(nl)
+        dids.copy_(nids)
+        out.fill_(-7)
+        graph.replay()
+        torch.cuda.synchronize()
+        ref = oracle.argmax_bf16(bits(nl))
+        ra, rb = oracle.accept(ncu.numpy(), ref, nids.numpy())
+        got = out.cpu().numpy()
+        t = nl.shape[0]
+        np.testing.assert_array_equal(got[:t], ref)
+        np.testing.assert_array_equal(got[t:t + 16], ra)
+        np.testing.assert_array_equal(got[t + 16:], rb)
+        # eager work between replays
+        K.argmax_accept(dl, dcu, dids)
+        torch.cuda.synchronize()
+
+
+def test_argmax_rows_with_index_map(K, cuda):
+    g = torch.Generator().manual_seed(4)
+    rows, vocab = 64, 32000
+    logits = torch.randn(rows, vocab, generator=g).to(torch.bfloat16)
+    d2t = torch.randint(-5, 100, (vocab,), generator=g)
+    out = K.argmax_rows(logits.to(cuda), d2t.to(cuda))
+    ref = oracle.argmax_bf16(bits(logits)).astype(np.int64)
+    np.testing.assert_array_equal(out.cpu().numpy(), ref + d2t.numpy()[ref])
+    out2 = K.argmax_rows(logits.to(cuda))
+    np.testing.assert_array_equal(out2.cpu().numpy(), ref)
+
+
+# ---------------------------------------------------------------- K2
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_store_kvcache_matches_oracle(K, cuda, fp8):
+    g = torch.Generator().manual_seed(21)
+    t, hq, hkv, d, nb, bs = 160, 16, 8, 128, 12, 256
+    # key/value as views into a fused QKV output (row stride > row)
+    qkv = (torch.randn(t, (hq + 2 * hkv) * d, generator=g) * 0.5).to(torch.bfloat16)
+    key = qkv[:, hq * d:(hq + hkv) * d].view(t, hkv, d)
+    value = qkv[:, (hq + hkv) * d:].view(t, hkv, d)
+    slots = torch.randperm(nb * bs, generator=g)[:t].to(torch.int32)
+    slots[::7] = -1
+    cdt = torch.float8_e4m3fn if fp8 else torch.bfloat16
+    init = (torch.randn(nb, bs, hkv, d, generator=g)).to(cdt)
+    kc, vc = init.clone().to(cuda), init.clone().to(cuda)
+    ks = torch.tensor([1.0], device=cuda) if fp8 else None
+    dq = qkv.to(cuda)
+    K.store_kvcache(dq[:, hq * d:(hq + hkv) * d].view(t, hkv, d),
+                    dq[:, (hq + hkv) * d:].view(t, hkv, d), kc, vc, slots.to(cuda), ks, ks)
+    rk, rv = bits(init).copy(), bits(init).copy()
+    oracle.store_kv(bits(key.contiguous()), bits(value.contiguous()), rk, rv, slots.numpy())
+    np.testing.assert_array_equal(bits(kc.cpu()), rk)
+    np.testing.assert_array_equal(bits(vc.cpu()), rv)
+
+
+def test_store_kvcache_fp8_scale_and_saturation(K, cuda):
+    vals = torch.tensor([0.0, -0.0, 1e-4, 0.0009765625, 0.0017, 0.3, -2.5, 447.0, 463.9, 464.0,
+                         465.0, 1e6, -1e6, float("inf"), float("-inf"), 240.0],
+                        dtype=torch.float32)
+    d = 128
+    row = torch.zeros(1, 1, d)
+    row[0, 0, :vals.numel()] = vals
+    key = row.to(torch.bfloat16)
+    value = (row * 0.5).to(torch.bfloat16)
+    kc = torch.zeros(1, 256, 1, d, dtype=torch.float8_e4m3fn, device=cuda)
+    vc = torch.zeros_like(kc)
+    slot = torch.tensor([5], dtype=torch.int32, device=cuda)
+    ks = torch.tensor([0.5], device=cuda)
+    vs = torch.tensor([2.0], device=cuda)
+    K.store_kvcache(key.to(cuda), value.to(cuda), kc, vc, slot, ks, vs)
+    rk = np.zeros((1, 256, 1, d), np.uint8)
+    rv = np.zeros((1, 256, 1, d), np.uint8)
+    oracle.store_kv(bits(key), bits(value), rk, rv, np.array([5], np.int32), 0.5, 2.0)
+    np.testing.assert_array_equal(bits(kc.cpu()), rk)
+    np.testing.assert_array_equal(bits(vc.cpu()), rv)
+
+
+@pytest.mark.parametrize("poison", [False, True])
+def test_rollback_matches_oracle(K, cuda, poison):
+    g = torch.Generator().manual_seed(8)
+    qs = [5, 5, 1, 6, 3]
+    cu = torch.tensor([0] + np.cumsum(qs).tolist(), dtype=torch.int32)
+    t = int(cu[-1])
+    acc = torch.tensor([0, 4, 0, 2, 7], dtype=torch.int32)   # 7 is clamped to q-1
+    slots = torch.randperm(4 * 256, generator=g)[:t].to(torch.int32)
+    lens = torch.tensor([900, 33, 12, 600, 70], dtype=torch.int32)
+    layers = 3
+    cache = torch.randn(2, layers, 4, 256, 2, 128, generator=g).to(torch.bfloat16)
+    dcache = cache.to(cuda)
+    dslots, dlens = slots.to(cuda), lens.to(cuda)
+    K.rollback(cu.to(cuda), acc.to(cuda), dslots, dlens, dcache[0], dcache[1], poison=poison)
+    rk, rv = bits(cache[0]).copy(), bits(cache[1]).copy()
+    rs, rl = slots.numpy(), lens.numpy()
+    for layer in range(layers):
+        s2, l2 = oracle.rollback(cu.numpy(), acc.numpy(), rs, rl, rk[layer], rv[layer], poison)
+    np.testing.assert_array_equal(dslots.cpu().numpy(), s2)
+    np.testing.assert_array_equal(dlens.cpu().numpy(), l2)
+    np.testing.assert_array_equal(bits(dcache[0].cpu()), rk)
+    np.testing.assert_array_equal(bits(dcache[1].cpu()), rv)
+
+
+# ---------------------------------------------------------------- K3
+
+def test_aux_gather_matches_oracle(K, cuda):
+    g = torch.Generator().manual_seed(13)
+    t, h = 384, 4096
+    hid = [(torch.randn(t, h, generator=g) * (10 ** i)).to(torch.bfloat16) for i in range(3)]
+    res = [(torch.randn(t, h, generator=g) * 3).to(torch.bfloat16) for _ in range(3)]
+    hid[1][5, :4] = torch.tensor([float("inf"), float("nan"), 1e38, -1e38])
+    res[1][5, :4] = torch.tensor([float("-inf"), 1.0, 1e38, -1e38])
+    src = torch.randint(0, t, (100,), generator=g).to(torch.int32)
+    src[3] = -1
+    out = K.aux_gather([x.to(cuda) for x in hid], [x.to(cuda) for x in res], src.to(cuda))
+    ref = oracle.aux_gather([bits(x) for x in hid], [bits(x) for x in res],
+                            np.maximum(src.numpy(), 0))
+    ref[3] = 0
+    np.testing.assert_array_equal(bits(out.cpu()), ref)
+
+
+# ---------------------------------------------------------------- K1
+
+def _run_verify(K, cuda, case, fp8=False):
+    kc = case["k_cache"].clone()
+    vc = case["v_cache"].clone()
+    if fp8:
+        kc = kc.float().to(torch.float8_e4m3fn)
+        vc = vc.float().to(torch.float8_e4m3fn)
+    dkc, dvc = kc.to(cuda), vc.to(cuda)
+    one = torch.ones(1, device=cuda) if fp8 else None
+    K.store_kvcache(case["k_new"].to(cuda), case["v_new"].to(cuda), dkc, dvc,
+                    case["slot_mapping"].to(cuda), one, one)
+    hq = case["q"].shape[1]
+    d = case["q"].shape[2]
+    out = K.paged_attention_varlen(
+        case["q"].to(cuda), dkc, dvc, case["cu_q"].to(cuda), case["cu_k"].to(cuda),
+        max(case["q_lens"]), int(case["lens"].max()), d ** -0.5, case["block_tables"].to(cuda),
+        k_scale=one, v_scale=one)
+    torch.cuda.synchronize()
+    # oracle: store then attention on the CPU copy
+    rk, rv = bits(kc).copy(), bits(vc).copy()
+    oracle.store_kv(bits(case["k_new"]), bits(case["v_new"]), rk, rv, case["slot_mapping"].numpy())
+    np.testing.assert_array_equal(bits(dkc.cpu()), rk)
+    ref = oracle.paged_attention(bits(case["q"]), rk, rv, case["cu_q"].numpy(),
+                                 case["lens"].numpy(), case["block_tables"].numpy(), d ** -0.5)
+    got = out.float().cpu().numpy()
+    return got, ref
+
+
+@pytest.mark.parametrize("name,kw", [
+    ("config2", dict(seed=1, batch=32, q_len=5, ctx_lo=512, ctx_hi=4096, hq=16, hkv=8)),
+    ("gqa4_k5", dict(seed=2, batch=6, q_len=6, ctx_lo=20, ctx_hi=1500, hq=32, hkv=8)),
+    ("gqa8_k7", dict(seed=3, batch=4, q_len=8, ctx_lo=8, ctx_hi=900, hq=64, hkv=8)),
+    ("ragged", dict(seed=4, batch=7, q_len=[1, 3, 6, 2, 5, 4, 1], ctx_lo=1, ctx_hi=700, hq=16,
+                    hkv=4)),
+    ("short", dict(seed=5, batch=5, q_len=3, ctx_lo=3, ctx_hi=40, hq=8, hkv=8)),
+])
+def test_verify_attention_bf16(K, cuda, name, kw):
+    got, ref = _run_verify(K, cuda, paged_case(**kw))
+    err = np.abs(got - ref).max()
+    assert err <= ATTN_TOL, (name, err)
+
+
+def test_verify_attention_fp8(K, cuda):
+    case = paged_case(seed=7, batch=8, q_len=5, ctx_lo=300, ctx_hi=3000, hq=16, hkv=8)
+    got, ref = _run_verify(K, cuda, case, fp8=True)
+    err = np.abs(got - ref).max()
+    assert err <= ATTN_TOL, err
+
+
+def test_fp8_decode_reference_geometry(K, cuda):
+    """The reference's FP8 test geometry (tests/test_fp8_kv_cache.py:20-41 of
+    the reference): 300 tokens, 2 blocks of 256 in table order [1, 0], 4 q /
+    2 kv heads, D=128.  Store -> page round trip is exact; decode matches the
+    fp32 einsum softmax within 2e-3; a captured graph re-reads a device-side
+    context length (113, then 300)."""
+    torch.manual_seed(0)
+    length, bs, hkv, hq, d = 300, 256, 2, 4, 128
+    key = (torch.randn(length, hkv, d) * 0.1).to(torch.bfloat16)
+    value = (torch.randn(length, hkv, d) * 0.1).to(torch.bfloat16)
+    kc = torch.empty(2, bs, hkv, d, dtype=torch.float8_e4m3fn, device=cuda)
+    vc = torch.empty_like(kc)
+    table = torch.tensor([[1, 0]], dtype=torch.int32, device=cuda)
+    pos = torch.arange(length, device=cuda)
+    slots = (table[0, pos // bs] * bs + pos % bs).to(torch.int32)
+    scale = torch.ones(1, device=cuda)
+    K.store_kvcache(key.to(cuda), value.to(cuda), kc, vc, slots, scale, scale)
+    qk = kc[table[0].long()].reshape(-1, hkv, d)[:length].cpu()
+    qv = vc[table[0].long()].reshape(-1, hkv, d)[:length].cpu()
+    np.testing.assert_array_equal(bits(qk), oracle.f32_to_e4m3(key.float().numpy()))
+    np.testing.assert_array_equal(bits(qv), oracle.f32_to_e4m3(value.float().numpy()))
+    query = (torch.randn(1, hq, d) * 0.1).to(torch.bfloat16)
+
+    def ref_for(n):
+        ek = qk[:n].float().repeat_interleave(hq // hkv, dim=1)
+        ev = qv[:n].float().repeat_interleave(hq // hkv, dim=1)
+        w = torch.softmax(torch.einsum("hd,lhd->hl", query[0].float(), ek) * d ** -0.5, -1)
+        return torch.einsum("hl,lhd->hd", w, ev)
+
+    actual = K.fp8_paged_decode_attention(query.to(cuda), kc, vc,
+                                          torch.tensor([length], dtype=torch.int32, device=cuda),
+                                          table, d ** -0.5, scale, scale)
+    assert (actual[0].float().cpu() - ref_for(length)).abs().max().item() <= FP8_TOL
+    # restated reference kernel agrees too
+    rest = oracle.fp8_paged_decode(bits(query), bits(kc.cpu()), bits(vc.cpu()),
+                                   np.array([length], np.int32), table.cpu().numpy(), d ** -0.5)
+    assert np.abs(rest[0] - ref_for(length).numpy()).max() <= FP8_TOL
+
+    ctx = torch.ones(1, dtype=torch.int32, device=cuda)
+    dq = query.to(cuda)
+    K.fp8_paged_decode_attention(dq, kc, vc, ctx, table, d ** -0.5, scale, scale)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        gout = K.fp8_paged_decode_attention(dq, kc, vc, ctx, table, d ** -0.5, scale, scale)
+    for n in (113, length, 1, 256):
+        ctx.fill_(n)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert (gout[0].float().cpu() - ref_for(n)).abs().max().item() <= FP8_TOL, n
+
+
+def test_decode_matches_varlen_single_row(K, cuda):
+    case = paged_case(seed=12, batch=9, q_len=1, ctx_lo=1, ctx_hi=2100, hq=32, hkv=8)
+    got, ref = _run_verify(K, cuda, case)
+    assert np.abs(got - ref).max() <= ATTN_TOL
+    # decode entry on the same cache state: identical math path
+    dkc = case["k_cache"].clone().to(cuda)
+    dvc = case["v_cache"].clone().to(cuda)
+    K.store_kvcache(case["k_new"].to(cuda), case["v_new"].to(cuda), dkc, dvc,
+                    case["slot_mapping"].to(cuda))
+    out = K.paged_attention_decode(case["q"].to(cuda), dkc, dvc, case["lens"].to(cuda),
+                                   case["block_tables"].to(cuda), 128 ** -0.5)
+    assert np.abs(out.float().cpu().numpy() - ref).max() <= ATTN_TOL
+
+
+def test_attention_skips_invalid_block_ids(K, cuda):
+    """Block-table entries outside [0, num_blocks) are treated as empty."""
+    case = paged_case(seed=14, batch=3, q_len=2, ctx_lo=300, ctx_hi=600, hq=8, hkv=2)
+    bt = case["block_tables"].clone()
+    nb = case["k_cache"].shape[0]
+    # first block of sequence 0 becomes invalid -> its keys are masked
+    bt[0, 0] = nb + 100
+    kc, vc = case["k_cache"].to(cuda), case["v_cache"].to(cuda)
+    out = K.paged_attention_varlen(case["q"].to(cuda), kc, vc, case["cu_q"].to(cuda),
+                                   case["cu_k"].to(cuda), 2, int(case["lens"].max()), 128 ** -0.5,
+                                   bt.to(cuda))
+    torch.cuda.synchronize()
+    # reference: mask = drop keys [0, 256) of sequence 0 by pointing them at
+    # an all-zero score... compute directly in numpy
+    q = case["q"].float().numpy()
+    kcf = case["k_cache"].float().numpy()
+    vcf = case["v_cache"].float().numpy()
+    L = int(case["lens"][0])
+    keys = np.stack([kcf[bt[0, n // 256], n % 256] if n >= 256 else np.zeros_like(kcf[0, 0])
+                     for n in range(L)])
+    vals = np.stack([vcf[bt[0, n // 256], n % 256] if n >= 256 else np.zeros_like(vcf[0, 0])
+                     for n in range(L)])
+    got = out.float().cpu().numpy()
+    for j in range(2):
+        vis = L - 2 + j + 1
+        for h in range(8):
+            s = keys[256:vis, h // 4] @ q[j, h] * 128 ** -0.5
+            w = np.exp(s - s.max())
+            w /= w.sum()
+            ref = w @ vals[256:vis, h // 4]
+            assert np.abs(got[j, h] - ref).max() <= ATTN_TOL

@@ -1,0 +1,282 @@
+"""Pins the CPU oracle against independent anchors (no GPU needed).
+
+Each oracle function is checked against something other than its own
+formula: torch's CPU kernels (argmax, bf16 and float8 casts, bf16 add, cat,
+index_select), hand-worked vectors written from the reference source
+(tests/golden/accept_cases.json), numpy dense attention with an explicit
+mask over pages gathered through the block table, and closed forms (one
+visible key, equal scores, round trips).
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from helpers import acceptance_logits, bits, from_bits, paged_case
+from oracle import oracle
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+# ---------------------------------------------------------------- argmax / accept
+
+def test_argmax_matches_torch_on_random_and_special_rows():
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(12, 3001, generator=g).to(torch.bfloat16)
+    xb = x.view(torch.int16)
+    x[0, 10] = 9.0
+    x[0, 2000] = 9.0
+    xb[1, 7] = 0x7FC1
+    xb[1, 3] = -64
+    x[2, :] = -1.0
+    x[2, 50] = -0.0
+    x[2, 60] = 0.0
+    x[3, :] = float("-inf")
+    x[4, :] = 0.0
+    x[5, 3000] = 100.0
+    x[6, 0] = float("inf")
+    x[6, 1] = float("inf")
+    x[7, :] = float("nan")
+    np.testing.assert_array_equal(oracle.argmax_bf16(bits(x)), x.argmax(-1).numpy())
+
+
+def test_argmax_brute_force_all_small_rows():
+    # every row over a 4-symbol alphabet including NaN / -0 / +0 / -inf
+    symbols = torch.tensor([float("nan"), -0.0, 0.0, float("-inf"), 1.0], dtype=torch.bfloat16)
+    idx = torch.cartesian_prod(*[torch.arange(5)] * 4)
+    rows = symbols[idx]
+    np.testing.assert_array_equal(oracle.argmax_bf16(bits(rows)), rows.argmax(-1).numpy())
+
+
+def test_accept_hand_worked_vectors():
+    cases = json.load(open(os.path.join(GOLDEN, "accept_cases.json")))["cases"]
+    for c in cases:
+        if "error" in c:
+            with pytest.raises(ValueError):
+                oracle.verify_greedy_proposals(c["proposal"], c["target"])
+            continue
+        v = oracle.verify_greedy_proposals(c["proposal"], c["target"])
+        assert v.accepted_count == c["accepted"]
+        assert v.accepted_tokens == c["tokens"]
+        assert v.replacement_token == c["replacement"]
+        if len(c["target"]) == len(c["proposal"]) + 1:
+            # the batched C restatement on the verify-row layout
+            q = len(c["target"])
+            ids = np.array([99] + c["proposal"], np.int64)
+            acc, bonus = oracle.accept(np.array([0, q], np.int32), np.array(c["target"], np.int32), ids)
+            assert acc[0] == c["accepted"] and bonus[0] == c["replacement"]
+
+
+def test_accept_batch_matches_python_restatement():
+    logits, cu_q, ids, prop = acceptance_logits(8, 4, 4096, 0.7, 0)
+    am = oracle.argmax_bf16(bits(logits))
+    acc, bonus = oracle.accept(cu_q.numpy(), am, ids.numpy())
+    for s in range(8):
+        target = am[s * 5:(s + 1) * 5].tolist()
+        v = oracle.verify_greedy_proposals(prop[s].tolist(), target)
+        assert acc[s] == v.accepted_count and bonus[s] == v.replacement_token
+    assert acc.max() > 0  # raised draft logits do get accepted
+    a2, b2, committed = oracle.reference_cpu_acceptance(logits, cu_q.tolist(), ids.tolist())
+    assert a2 == acc.tolist() and b2 == bonus.tolist()
+    assert committed == int(acc.sum()) + 8
+
+
+def test_accept_empty_sequence():
+    acc, bonus = oracle.accept(np.array([0, 0, 2], np.int32), np.array([4, 5], np.int32),
+                               np.array([1, 4], np.int64))
+    assert acc.tolist() == [0, 1] and bonus.tolist() == [-1, 5]
+
+
+# ---------------------------------------------------------------- conversions
+
+def test_e4m3_decode_all_codes_match_torch():
+    codes = np.arange(256, dtype=np.uint8)
+    ref = torch.from_numpy(codes).view(torch.float8_e4m3fn).float().numpy()
+    got = oracle.e4m3_to_f32(codes)
+    nan = np.isnan(ref)
+    assert np.array_equal(nan, np.isnan(got))
+    np.testing.assert_array_equal(got[~nan], ref[~nan])
+
+
+def test_e4m3_encode_every_bf16_matches_torch_in_range():
+    pat = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    x = oracle.bf16_bits_to_f32(pat)
+    got = oracle.f32_to_e4m3(x)
+    ref = torch.from_numpy(x).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    finite_small = np.isfinite(x) & (np.abs(x) < 464.0)
+    np.testing.assert_array_equal(got[finite_small], ref[finite_small])
+    # NaN keeps its sign; everything else saturates to +-448 (0x7E)
+    nan = np.isnan(x)
+    assert np.all((got[nan] & 0x7F) == 0x7F)
+    big = ~nan & ~finite_small
+    assert np.all((got[big] & 0x7F) == 0x7E)
+    assert np.all((got[big] >> 7) == (x[big] < 0))
+
+
+def test_e4m3_encode_ties_round_to_even():
+    # midpoints between adjacent codes round to the even code
+    for c in range(0, 0x7D):
+        a = float(oracle.e4m3_to_f32(np.array([c], np.uint8))[0])
+        b = float(oracle.e4m3_to_f32(np.array([c + 1], np.uint8))[0])
+        mid = np.float32((a + b) / 2)
+        want = c if c % 2 == 0 else c + 1
+        assert oracle.f32_to_e4m3(np.array([mid]))[0] == want, c
+    x = torch.randn(20000, generator=torch.Generator().manual_seed(1)) * 30
+    got = oracle.f32_to_e4m3(x.numpy())
+    ref = x.to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_bf16_rounding_matches_torch():
+    g = torch.Generator().manual_seed(2)
+    x = torch.cat([torch.randn(5000, generator=g) * 10.0 ** e for e in (-30, -3, 0, 3, 30)])
+    x = torch.cat([x, torch.tensor([float("inf"), float("-inf"), 3.3895314e38, -0.0, 1e-45])])
+    np.testing.assert_array_equal(oracle.f32_to_bf16_bits(x.numpy()), bits(x.to(torch.bfloat16)))
+
+
+# ---------------------------------------------------------------- store / rollback
+
+@pytest.mark.parametrize("fp8", [False, True])
+def test_store_kv_round_trip(fp8):
+    g = torch.Generator().manual_seed(3)
+    t, hkv, d, nb, bs = 40, 2, 16, 3, 32
+    key = (torch.randn(t, hkv, d, generator=g) * 0.5).to(torch.bfloat16)
+    val = (torch.randn(t, hkv, d, generator=g) * 0.5).to(torch.bfloat16)
+    slots = torch.randperm(nb * bs, generator=g)[:t].to(torch.int32)
+    slots[3] = -1
+    slots[5] = nb * bs + 7        # out of range: skipped
+    dt = np.uint8 if fp8 else np.uint16
+    kc = np.full((nb, bs, hkv, d), 0x11, dt)
+    vc = np.full((nb, bs, hkv, d), 0x11, dt)
+    oracle.store_kv(bits(key), bits(val), kc, vc, slots.numpy())
+    flat_k = kc.reshape(nb * bs, hkv, d)
+    flat_v = vc.reshape(nb * bs, hkv, d)
+    for i in range(t):
+        s = int(slots[i])
+        if s < 0 or s >= nb * bs:
+            continue
+        if fp8:
+            ref_k = key[i].float().to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+            ref_v = val[i].float().to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+        else:
+            ref_k, ref_v = bits(key[i]), bits(val[i])
+        np.testing.assert_array_equal(flat_k[s], ref_k)
+        np.testing.assert_array_equal(flat_v[s], ref_v)
+    written = {int(s) for s in slots if 0 <= int(s) < nb * bs}
+    untouched = [s for s in range(nb * bs) if s not in written]
+    assert np.all(flat_k[untouched] == 0x11)
+
+
+def test_rollback_hand_case():
+    cu = np.array([0, 5, 6, 9], np.int32)
+    acc = np.array([2, 0, -3], np.int32)        # -3 clamps to 0
+    slots = np.arange(9, dtype=np.int32) + 100
+    lens = np.array([50, 7, 30], np.int32)
+    kc = np.ones((1, 256, 1, 4), np.uint16)
+    vc = np.ones((1, 256, 1, 4), np.uint16)
+    s2, l2 = oracle.rollback(cu, acc, slots, lens, kc, vc, poison=True)
+    assert s2.tolist() == [100, 101, 102, -1, -1, 105, 106, -1, -1]
+    assert l2.tolist() == [48, 7, 28]
+    zeroed = [103, 104, 107, 108]
+    assert np.all(kc[0, zeroed] == 0) and np.all(vc[0, zeroed] == 0)
+    assert np.all(np.delete(kc[0], zeroed, axis=0) == 1)
+
+
+# ---------------------------------------------------------------- aux gather
+
+def test_aux_gather_matches_torch():
+    g = torch.Generator().manual_seed(4)
+    t, h = 30, 64
+    hid = [(torch.randn(t, h, generator=g) * 10 ** i).to(torch.bfloat16) for i in range(3)]
+    res = [(torch.randn(t, h, generator=g) * 10 ** (2 - i)).to(torch.bfloat16) for i in range(3)]
+    hid[0][1, 0] = float("inf")
+    res[0][1, 0] = float("-inf")
+    src = torch.tensor([4, 0, 29, 4, 17], dtype=torch.int32)
+    ref = torch.cat([a + b for a, b in zip(hid, res)], dim=-1).index_select(0, src.long())
+    got = oracle.aux_gather([bits(a) for a in hid], [bits(b) for b in res], src.numpy())
+    np.testing.assert_array_equal(got, bits(ref))
+
+
+# ---------------------------------------------------------------- attention
+
+def _dense_reference(case, q_bits=None):
+    """numpy dense attention: gather each sequence's pages into a contiguous
+    [L, Hkv, D] matrix first, then softmax(QK^T + mask) V with an explicit
+    bottom-right causal mask -- a different code path from the oracle."""
+    bs = case["block_size"]
+    q = case["q"].double().numpy()
+    kc = case["k_cache"].double().numpy()
+    vc = case["v_cache"].double().numpy()
+    hq, hkv = q.shape[1], kc.shape[2]
+    out = np.zeros(q.shape)
+    for i, (L, qn) in enumerate(zip(case["lens"].tolist(), case["q_lens"])):
+        blocks = case["block_tables"][i, :(L + bs - 1) // bs].long().numpy()
+        k = kc[blocks].reshape(-1, hkv, q.shape[2])[:L]
+        v = vc[blocks].reshape(-1, hkv, q.shape[2])[:L]
+        s0 = int(case["cu_q"][i])
+        rows = np.arange(qn)[:, None]
+        cols = np.arange(L)[None, :]
+        mask = cols <= (L - qn + rows)
+        for h in range(hq):
+            sc = q[s0:s0 + qn, h] @ k[:, h // (hq // hkv)].T * q.shape[2] ** -0.5
+            sc = np.where(mask, sc, -np.inf)
+            w = np.exp(sc - sc.max(-1, keepdims=True))
+            w /= w.sum(-1, keepdims=True)
+            out[s0:s0 + qn, h] = w @ v[:, h // (hq // hkv)]
+    return out
+
+
+@pytest.mark.parametrize("kw", [
+    dict(seed=1, batch=3, q_len=5, ctx_lo=5, ctx_hi=600, hq=4, hkv=2, head_dim=32, block_size=64),
+    dict(seed=2, batch=4, q_len=[1, 2, 7, 3], ctx_lo=1, ctx_hi=300, hq=8, hkv=1, head_dim=16,
+         block_size=32),
+])
+def test_paged_attention_matches_dense_numpy(kw):
+    case = paged_case(**kw)
+    got = oracle.paged_attention(bits(case["q"]), bits(case["k_cache"]), bits(case["v_cache"]),
+                                 case["cu_q"].numpy(), case["lens"].numpy(),
+                                 case["block_tables"].numpy(), case["q"].shape[2] ** -0.5)
+    ref = _dense_reference(case)
+    assert np.abs(got - ref).max() < 1e-6
+
+
+def test_paged_attention_closed_forms():
+    # one visible key -> output equals that value row; equal scores -> mean
+    d, bs = 8, 32
+    q = torch.zeros(2, 1, d).to(torch.bfloat16)
+    q[0, 0, 0] = 1.0
+    kc = torch.zeros(2, bs, 1, d)
+    vc = torch.arange(2 * bs * d, dtype=torch.float32).reshape(2, bs, 1, d) / 64
+    bt = np.array([[1, 0]], np.int32)
+    # sequence of 3 keys, 2 query rows: row 0 sees keys 0..1, row 1 sees 0..2
+    out = oracle.paged_attention(bits(q), bits(kc.to(torch.bfloat16)), bits(vc.to(torch.bfloat16)),
+                                 np.array([0, 2], np.int32), np.array([3], np.int32), bt, 1.0)
+    vb = vc.to(torch.bfloat16).float().numpy()
+    np.testing.assert_allclose(out[0, 0], vb[1, 0:2, 0].mean(0), rtol=1e-6)
+    np.testing.assert_allclose(out[1, 0], vb[1, 0:3, 0].mean(0), rtol=1e-6)
+    # L=1, q=1 -> exactly the single value row
+    out1 = oracle.paged_attention(bits(q[:1]), bits(kc.to(torch.bfloat16)),
+                                  bits(vc.to(torch.bfloat16)), np.array([0, 1], np.int32),
+                                  np.array([1], np.int32), bt, 1.0)
+    np.testing.assert_array_equal(out1[0, 0], vb[1, 0, 0])
+
+
+def test_fp8_decode_restatement_within_reference_bound():
+    torch.manual_seed(0)
+    length, bs, hkv, hq, d = 300, 256, 2, 4, 128
+    key = (torch.randn(length, hkv, d) * 0.1).to(torch.bfloat16)
+    val = (torch.randn(length, hkv, d) * 0.1).to(torch.bfloat16)
+    kc = np.zeros((2, bs, hkv, d), np.uint8)
+    vc = np.zeros((2, bs, hkv, d), np.uint8)
+    table = np.array([[1, 0]], np.int32)
+    pos = np.arange(length)
+    slots = (table[0, pos // bs] * bs + pos % bs).astype(np.int32)
+    oracle.store_kv(bits(key), bits(val), kc, vc, slots)
+    q = (torch.randn(1, hq, d) * 0.1).to(torch.bfloat16)
+    for n in (1, 113, 300):
+        got = oracle.fp8_paged_decode(bits(q), kc, vc, np.array([n], np.int32), table, d ** -0.5)
+        ref = oracle.paged_attention(bits(q), kc, vc, np.array([0, 1], np.int32),
+                                     np.array([n], np.int32), table, d ** -0.5)
+        assert np.abs(got - ref).max() <= 2e-3
