@@ -9,8 +9,9 @@
 // first index of the maximum, with NaN as the maximum -- torch.argmax's rule.
 // The last block of a row (device-scope counter) merges the chunk keys; the
 // last row of a sequence (second counter) runs the accept scan.  Both counters
-// reset themselves, so the workspace stays zero-filled between calls and the
-// kernel is safe to replay from a HIP graph.
+// reset themselves and the merged partials are cleared, so the workspace is
+// zero-filled again after every call, whatever its shape, and the kernel is
+// safe to replay from a HIP graph.
 #include "common.h"
 
 namespace nva {
@@ -117,8 +118,13 @@ argmax_kernel(const uint16_t* __restrict__ logits, int64_t row_stride, int32_t v
     if (!flag) return;
     __threadfence();
     uint64_t k = 0;
-    for (int32_t c = threadIdx.x; c < chunks; c += kThreads)
-      k = umax64(k, load_relaxed_agent(partials + static_cast<int64_t>(row) * chunks + c));
+    for (int32_t c = threadIdx.x; c < chunks; c += kThreads) {
+      uint64_t* slot = partials + static_cast<int64_t>(row) * chunks + c;
+      k = umax64(k, load_relaxed_agent(slot));
+      // leave the whole workspace zero-filled: a later call with another
+      // shape may place its counters where these partials were
+      store_relaxed_agent(slot, static_cast<uint64_t>(0));
+    }
     key = block_max(k, red);
     if (threadIdx.x == 0) store_relaxed_agent(row_cnt + row, 0u);
   }
