@@ -1,9 +1,11 @@
 // K1: paged verify attention for gfx950 (MFMA 16x16x32 bf16).
 //
 // Work decomposition: one 256-thread workgroup (4 waves) per
-// (kv split, kv head, sequence).  The query tile of a workgroup is the
-// q_i * G query rows that share the kv head (G = Hq / Hkv), padded to NT*16
-// columns (NT = 1..4).  The key range of the split is walked in 32-key chunks,
+// (query tile, kv split, kv head, sequence).  A query tile is up to 64/G
+// consecutive query positions of one sequence times the G query heads that
+// share the kv head (G = Hq / Hkv), padded to NT*16 columns (NT = 1..4); a
+// verify step (k+1 positions, G <= 64/(k+1)) is a single tile, a prefill is
+// many.  Each tile only walks the keys its last row can see.  The key range of the split is walked in 32-key chunks,
 // chunk c by wave c % 4, each wave keeping its own online-softmax state.
 //
 // Per 32-key chunk a wave computes S^T = K . Q^T (two 16-key tiles, MFMA with
@@ -65,6 +67,7 @@ struct AttnParams {
   float* ws_o;
   float* ws_lse;
   int32_t split_len, max_splits;
+  int32_t qtile, n_qtiles;                            // query positions per workgroup
 };
 
 __device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -113,7 +116,8 @@ __global__ void __launch_bounds__(kThreads)
 paged_attention_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsDwords];
 
-  const int split = blockIdx.x;
+  const int split = blockIdx.x % p.max_splits;
+  const int qt = blockIdx.x / p.max_splits;
   const int kvh = blockIdx.y;
   const int seq = blockIdx.z;
   const int wave = threadIdx.x / kWave;
@@ -123,24 +127,29 @@ paged_attention_kernel(AttnParams p) {
 
   int q_start, q_len, L;
   seq_geometry(p, seq, q_start, q_len, L);
-  if (q_len <= 0) return;
-  const int rows = q_len * p.group;
+  // this workgroup's query positions: j0 .. j0 + jn - 1 of the sequence
+  const int j0 = qt * p.qtile;
+  const int jn = (q_len - j0 < p.qtile) ? q_len - j0 : p.qtile;
+  if (jn <= 0) return;
+  const int rows = jn * p.group;
+  // keys any row of the tile can see (bottom-right causal)
+  const int kv_limit = L - q_len + j0 + jn;
   const int kv_begin = split * p.split_len;
-  if (L <= 0) {
+  if (kv_limit <= 0) {
     // nothing visible: zero output rows (once, from split 0)
     if (split != 0) return;
     for (int idx = threadIdx.x; idx < rows * (kD / 8); idx += kThreads) {
       const int n = idx / (kD / 8), dv = idx % (kD / 8);
-      const int j = n / p.group, hh = n % p.group;
+      const int j = j0 + n / p.group, hh = n % p.group;
       uint16_t* o = p.out + static_cast<int64_t>(q_start + j) * p.out_row_stride +
                     static_cast<int64_t>(kvh * p.group + hh) * p.out_head_stride + dv * 8;
       *reinterpret_cast<uint4*>(o) = make_uint4(0, 0, 0, 0);
     }
     return;
   }
-  if (kv_begin >= L) return;
-  const int kv_end = kv_begin + p.split_len < L ? kv_begin + p.split_len : L;
-  const int nsplit = (L + p.split_len - 1) / p.split_len;
+  if (kv_begin >= kv_limit) return;
+  const int kv_end = kv_begin + p.split_len < kv_limit ? kv_begin + p.split_len : kv_limit;
+  const int nsplit = (kv_limit + p.split_len - 1) / p.split_len;
 
   float kscale = 1.0f, vscale = 1.0f;
   if (FP8) {
@@ -156,7 +165,7 @@ paged_attention_kernel(AttnParams p) {
   for (int nt = 0; nt < NT; ++nt) {
     const int n = nt * 16 + m16;
     if (n < rows) {
-      const int j = n / p.group, hh = n % p.group;
+      const int j = j0 + n / p.group, hh = n % p.group;
       const uint16_t* qp = p.q + static_cast<int64_t>(q_start + j) * p.q_row_stride +
                            static_cast<int64_t>(kvh * p.group + hh) * p.q_head_stride;
 #pragma unroll
@@ -199,7 +208,7 @@ paged_attention_kernel(AttnParams p) {
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
       int key = kb + kt * 16 + m16;
-      key = key < L ? key : L - 1;
+      key = key < kv_limit ? key : kv_limit - 1;
       const int64_t e = blk_base + static_cast<int64_t>(off0 + key - kb) * p.tok_stride;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
@@ -217,7 +226,7 @@ paged_attention_kernel(AttnParams p) {
       for (int i = 0; i < 4; ++i) {
         const int r = 8 * i + (lane >> 3);
         int key = kb + r;
-        key = key < L ? key : L - 1;
+        key = key < kv_limit ? key : kv_limit - 1;
         const int64_t e = blk_base + static_cast<int64_t>(off0 + key - kb) * p.tok_stride + (lane & 7) * 16;
         const uint4 w = *reinterpret_cast<const uint4*>(p.v_cache + e);
         const bf16x8_t a = fp8x8_to_bf16(make_uint2(w.x, w.y));
@@ -231,7 +240,7 @@ paged_attention_kernel(AttnParams p) {
       for (int i = 0; i < 8; ++i) {
         const int r = 4 * i + g;
         int key = kb + r;
-        key = key < L ? key : L - 1;
+        key = key < kv_limit ? key : kv_limit - 1;
         const int64_t e = blk_base + static_cast<int64_t>(off0 + key - kb) * p.tok_stride + m16 * 8;
         const uint4 w = *reinterpret_cast<const uint4*>(p.v_cache + e * 2);
         *reinterpret_cast<uint4*>(vst + r * kVPitch + m16 * 4) = w;
@@ -397,7 +406,7 @@ paged_attention_kernel(AttnParams p) {
         for (int w = 0; w < kWaves; ++w) s += sacc_lds[(w * 16 + ccol) * kAccPitch + dgrp * 8 + k];
         o[k] = ltot > 0.0f ? s / ltot * vscale : 0.0f;
       }
-      const int j = n / p.group, hh = n % p.group;
+      const int j = j0 + n / p.group, hh = n % p.group;
       const int t = q_start + j;
       const int h = kvh * p.group + hh;
       if (nsplit == 1) {
@@ -438,8 +447,13 @@ combine_kernel(AttnParams p) {
   }
   int q_start, q_len, L;
   seq_geometry(p, seq, q_start, q_len, L);
-  if (t - q_start >= q_len) return;
-  const int nsplit = (L + p.split_len - 1) / p.split_len;
+  const int j = t - q_start;
+  if (j >= q_len) return;
+  // the split count of this row's query tile (same rule as the main kernel)
+  const int j0 = j / p.qtile * p.qtile;
+  const int jn = (q_len - j0 < p.qtile) ? q_len - j0 : p.qtile;
+  const int kv_limit = L - q_len + j0 + jn;
+  const int nsplit = kv_limit > 0 ? (kv_limit + p.split_len - 1) / p.split_len : 0;
   if (nsplit <= 1) return;
   const int64_t base = (static_cast<int64_t>(t) * p.hq + h) * p.max_splits;
   float M = -INFINITY;
@@ -459,9 +473,17 @@ combine_kernel(AttnParams p) {
   *reinterpret_cast<uint32_t*>(op) = pack_bf16(o0 * inv, o1 * inv);
 }
 
-void choose_split(int32_t num_seqs, int32_t num_kv_heads, int32_t max_k, int32_t* split_len,
-                  int32_t* max_splits) {
-  const int64_t base = static_cast<int64_t>(num_seqs > 0 ? num_seqs : 1) * (num_kv_heads > 0 ? num_kv_heads : 1);
+// query positions per workgroup: as many as fit 64 tile rows (>= 1)
+int32_t choose_qtile(int32_t max_q, int32_t group) {
+  int32_t qtile = group > 0 ? 64 / group : 1;
+  qtile = qtile < 1 ? 1 : qtile;
+  return max_q < qtile ? (max_q > 0 ? max_q : 1) : qtile;
+}
+
+void choose_split(int32_t num_seqs, int32_t num_kv_heads, int32_t n_qtiles, int32_t max_k,
+                  int32_t* split_len, int32_t* max_splits) {
+  const int64_t base = static_cast<int64_t>(num_seqs > 0 ? num_seqs : 1) *
+                       (num_kv_heads > 0 ? num_kv_heads : 1) * (n_qtiles > 0 ? n_qtiles : 1);
   int64_t want = (kTargetWorkgroups + base - 1) / base;
   const int32_t mk = max_k > 1 ? max_k : 1;
   int64_t by_len = (mk + kMinSplit - 1) / kMinSplit;
@@ -473,9 +495,12 @@ void choose_split(int32_t num_seqs, int32_t num_kv_heads, int32_t max_k, int32_t
   *max_splits = (mk + len - 1) / len;
 }
 
-size_t workspace_bytes(int32_t num_seqs, int32_t num_tokens, int32_t hq, int32_t hkv, int32_t max_k) {
+size_t workspace_bytes(int32_t num_seqs, int32_t num_tokens, int32_t hq, int32_t hkv, int32_t max_q,
+                       int32_t max_k) {
+  const int32_t qtile = choose_qtile(max_q, hkv > 0 ? hq / hkv : 1);
+  const int32_t n_qtiles = (max_q + qtile - 1) / qtile;
   int32_t len, ms;
-  choose_split(num_seqs, hkv, max_k, &len, &ms);
+  choose_split(num_seqs, hkv, n_qtiles, max_k, &len, &ms);
   if (ms <= 1) return 0;
   const size_t slots = static_cast<size_t>(num_tokens) * hq * ms;
   return slots * kD * sizeof(float) + slots * sizeof(float) + 256;
@@ -498,17 +523,19 @@ int run_attention(AttnParams& p, int kv_dtype, void* workspace, size_t workspace
   if (p.block_size <= 0 || p.block_size % kChunk != 0 || p.num_blocks <= 0) return NVA_ERR_UNSUPPORTED;
   if (p.bt_cols < 0 || p.bt_stride < p.bt_cols) return NVA_ERR_ARG;
   p.group = p.hq / p.hkv;
-  const int tile_rows = p.max_q * p.group;
-  if (tile_rows > 64) return NVA_ERR_UNSUPPORTED;
+  if (p.group > 64) return NVA_ERR_UNSUPPORTED;
+  p.qtile = choose_qtile(p.max_q, p.group);
+  p.n_qtiles = (p.max_q + p.qtile - 1) / p.qtile;
+  const int tile_rows = p.qtile * p.group;
   // alignment of 16-byte vector accesses
   const int64_t vec_elems = kv_dtype == NVA_KV_BF16 ? 8 : 16;
   if (!aligned16(p.q) || !aligned16(p.out) || !aligned16(p.k_cache) || !aligned16(p.v_cache) ||
       p.q_row_stride % 8 || p.q_head_stride % 8 || p.out_row_stride % 8 || p.out_head_stride % 8 ||
       p.blk_stride % vec_elems || p.tok_stride % vec_elems || p.head_stride % vec_elems)
     return NVA_ERR_UNSUPPORTED;
-  choose_split(p.num_seqs, p.hkv, p.max_k, &p.split_len, &p.max_splits);
+  choose_split(p.num_seqs, p.hkv, p.n_qtiles, p.max_k, &p.split_len, &p.max_splits);
   if (p.max_splits > 1) {
-    const size_t need = workspace_bytes(p.num_seqs, p.num_tokens, p.hq, p.hkv, p.max_k);
+    const size_t need = workspace_bytes(p.num_seqs, p.num_tokens, p.hq, p.hkv, p.max_q, p.max_k);
     if (!workspace || workspace_bytes_ < need || !aligned16(workspace)) return NVA_ERR_WORKSPACE;
     const size_t slots = static_cast<size_t>(p.num_tokens) * p.hq * p.max_splits;
     p.ws_o = static_cast<float*>(workspace);
@@ -518,7 +545,7 @@ int run_attention(AttnParams& p, int kv_dtype, void* workspace, size_t workspace
     p.ws_lse = nullptr;
   }
   const bool fp8 = kv_dtype == NVA_KV_FP8_E4M3;
-  dim3 grid(p.max_splits, p.hkv, p.num_seqs);
+  dim3 grid(p.max_splits * p.n_qtiles, p.hkv, p.num_seqs);
   const int nt = (tile_rows + 15) / 16;
   if (nt <= 1)
     launch_nt<1>(p, fp8, grid, s);
@@ -541,10 +568,13 @@ using namespace nva;
 
 extern "C" size_t nva_paged_attention_workspace_size(int32_t num_seqs, int32_t num_tokens,
                                                      int32_t num_q_heads, int32_t num_kv_heads,
-                                                     int32_t head_dim, int32_t max_seqlen_k) {
-  if (num_seqs <= 0 || num_tokens <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim != kD)
+                                                     int32_t head_dim, int32_t max_seqlen_q,
+                                                     int32_t max_seqlen_k) {
+  if (num_seqs <= 0 || num_tokens <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 || head_dim != kD ||
+      max_seqlen_q <= 0)
     return 0;
-  return workspace_bytes(num_seqs, num_tokens, num_q_heads, num_kv_heads, max_seqlen_k);
+  return workspace_bytes(num_seqs, num_tokens, num_q_heads, num_kv_heads, max_seqlen_q,
+                         max_seqlen_k);
 }
 
 extern "C" int nva_paged_attention_varlen(

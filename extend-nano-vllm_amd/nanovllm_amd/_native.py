@@ -41,13 +41,18 @@ SIGNATURES = {
     "nva_argmax_workspace_size": (_SZ, [_I32, _I32, _I32]),
     "nva_argmax_accept": (_INT, [_P, _I64, _I32, _P, _I32, _I32, _P, _P, _P, _P, _P, _SZ, _P]),
     "nva_argmax_rows": (_INT, [_P, _I64, _I32, _I32, _P, _P, _P, _SZ, _P]),
-    "nva_paged_attention_workspace_size": (_SZ, [_I32, _I32, _I32, _I32, _I32, _I32]),
+    "nva_paged_attention_workspace_size": (_SZ, [_I32, _I32, _I32, _I32, _I32, _I32, _I32]),
     "nva_paged_attention_varlen": (_INT, [_P, _I64, _I64, _P, _P, _INT, _I64, _I64, _I64, _I32,
                                           _I32, _P, _P, _P, _I64, _I32, _I32, _I32, _I32, _I32,
                                           _I32, _I32, _I32, _F32, _P, _P, _P, _I64, _I64, _P, _SZ, _P]),
     "nva_paged_attention_decode": (_INT, [_P, _I64, _I64, _P, _P, _INT, _I64, _I64, _I64, _I32,
                                           _I32, _P, _P, _I64, _I32, _I32, _I32, _I32, _I32, _I32, _F32,
                                           _P, _P, _P, _I64, _I64, _P, _SZ, _P]),
+    "nva_rms_norm": (_INT, [_P, _I64, _P, _P, _I64, _I32, _I32, _F32, _P]),
+    "nva_add_rms_norm": (_INT, [_P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _I32, _I32, _F32, _P]),
+    "nva_qk_norm_rope": (_INT, [_P, _I64, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _F32, _P,
+                                _P, _P]),
+    "nva_silu_mul": (_INT, [_P, _I64, _P, _I64, _I32, _I32, _P]),
 }
 
 

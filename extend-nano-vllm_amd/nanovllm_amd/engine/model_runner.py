@@ -1,0 +1,509 @@
+"""Runs the target and EAGLE3 draft models on one GPU
+(nanovllm/engine/model_runner.py, the single-process EAGLE3 subset).
+
+Method names and return values follow the reference so the engine-level
+orchestration is unchanged: ``run``, ``propose_eagle3_batch``,
+``verify_eagle3_batch``, ``commit_eagle3``, ``release_eagle3_state``,
+``get_eagle3_runtime_capabilities``, ``run_eagle3_graph``, ``call``.
+The engine's hot path uses the batched forms ``verify_eagle3_batch_fused``
+(argmax + accept fused on the GPU, one device->host copy per step) and
+``commit_eagle3_batch`` (one ragged draft forward for every sequence's
+committed tail instead of one forward per token per sequence).
+
+Draft KV slots.  The draft consumes the pair (token[p+1], target aux state
+at p) at RoPE position p and stores its K/V at the slot of position p, in
+prefill, proposal and commit alike.  (The reference stores decode- and
+commit-time draft K/V one slot later than prefill, model_runner.py:
+1087-1096 / :1143-1149 vs :784-789, leaving one slot unwritten but read;
+emitted tokens do not depend on it because the target verifies every
+token.)
+"""
+from __future__ import annotations
+
+import torch
+
+from nanovllm_amd import _native
+from nanovllm_amd import kernels as K
+from nanovllm_amd.context import get_context, reset_context, set_context
+from nanovllm_amd.eagle3 import Eagle3KVCache, load_eagle3_model
+from nanovllm_amd.engine.sequence import Sequence
+from nanovllm_amd.layers import Attention, init_random_, param_bytes
+from nanovllm_amd.loader import load_model
+from nanovllm_amd.qwen3 import Qwen3ForCausalLM, aux_concat
+
+
+def _pinned(values, dtype) -> torch.Tensor:
+    return torch.tensor(values, dtype=dtype, pin_memory=True)
+
+
+class ModelRunner:
+
+    def __init__(self, config, rank: int = 0, event=None):
+        if rank != 0:
+            raise ValueError("this build runs one process per GPU (rank 0 only)")
+        _native.load()   # fail loudly without the HIP library
+        self.config = config
+        hf = config.hf_config
+        self.block_size = config.kvcache_block_size
+        self.enforce_eager = config.enforce_eager
+        self.rank = rank
+        self.device = torch.device("cuda", config.device_offset)
+        torch.cuda.set_device(self.device)
+        self._exited = False
+        self.decode_graph_replay_count = 0
+        default_dtype = torch.get_default_dtype()
+        dtype = getattr(hf, "torch_dtype", None) or getattr(hf, "dtype", None) or torch.bfloat16
+        if isinstance(dtype, str):
+            dtype = getattr(torch, dtype)
+        self.dtype = dtype
+        torch.set_default_dtype(dtype)
+        torch.set_default_device(self.device)
+        try:
+            self.model = Qwen3ForCausalLM(hf)
+            if config.load_format == "dummy":
+                init_random_(self.model, config.seed)
+            else:
+                load_model(self.model, config.model)
+            self.model.eval()
+            self.speculative_config = config.speculative_config
+            self.eagle3_model = None
+            self.eagle3_states: dict[int, Eagle3KVCache] = {}
+            self.eagle_graphs: dict = {}
+            self.eagle_graph_vars: dict = {}
+            self.graphs: dict = {}
+            self._pending_verify = None
+            if self.speculative_config is not None:
+                self.eagle3_model = load_eagle3_model(self.speculative_config.model, self.device,
+                                                      config.load_format, config.seed + 1)
+                ec = self.eagle3_model.config
+                if ec.target_hidden_size != hf.hidden_size or ec.target_vocab_size != hf.vocab_size:
+                    raise ValueError("EAGLE3 checkpoint is incompatible with the target Qwen3")
+                if ec.num_aux_hidden_states != len(self.speculative_config.aux_hidden_state_layers):
+                    raise ValueError("EAGLE3 aux state count does not match aux_hidden_state_layers")
+            self.warmup_model()
+            self.allocate_kv_cache()
+        finally:
+            torch.set_default_device("cpu")
+            torch.set_default_dtype(default_dtype)
+        # benchmarks may ask to keep the last verify's logits and inputs
+        self.keep_verify_inputs = False
+        self.last_verify_inputs = None
+        # one pinned host buffer receives argmax + accept results each verify
+        self._verify_host = torch.empty(1 << 16, dtype=torch.int32, pin_memory=True)
+        self._verify_dev = torch.empty(1 << 16, dtype=torch.int32, device=self.device)
+
+    # ------------------------------------------------------------ RPC surface
+
+    def call(self, method_name: str, *args):
+        method = getattr(self, method_name, None)
+        if method is None:
+            raise AttributeError(f"ModelRunner has no method {method_name!r}")
+        return method(*args)
+
+    def exit(self):
+        if self._exited:
+            return
+        self._exited = True
+        self.graphs.clear()
+        self.eagle_graphs.clear()
+        self.eagle_graph_vars.clear()
+        torch.cuda.synchronize(self.device)
+
+    # ------------------------------------------------------------ memory
+
+    @torch.inference_mode()
+    def warmup_model(self):
+        """One dummy prefill (attention returns zeros) at the largest batch to
+        measure peak activation memory before sizing the KV cache."""
+        torch.cuda.empty_cache()
+        torch.cuda.reset_peak_memory_stats(self.device)
+        n = max(1, min(self.config.max_num_batched_tokens, self.config.max_model_len))
+        ids = torch.zeros(n, dtype=torch.int64, device=self.device)
+        pos = torch.arange(n, dtype=torch.int64, device=self.device)
+        set_context(True)
+        get_context().is_dummy = True
+        try:
+            if self.speculative_config is not None:
+                hidden, aux = self.model.forward_with_aux_hidden_states(
+                    ids, pos, self.speculative_config.aux_hidden_state_layers)
+                combined = self.eagle3_model.combine_hidden_states(aux_concat(aux))
+                self.eagle3_model.forward_with_cache(ids, pos, combined)
+            else:
+                hidden = self.model(ids, pos)
+            self.model.compute_logits(hidden[-1:])
+        finally:
+            reset_context()
+        torch.cuda.synchronize(self.device)
+        torch.cuda.empty_cache()
+
+    def _kv_dtype(self):
+        return torch.float8_e4m3fn if self.config.kv_cache_dtype == "fp8" else self.dtype
+
+    def allocate_kv_cache(self):
+        config = self.config
+        hf = config.hf_config
+        kv_dtype = self._kv_dtype()
+        head_dim = getattr(hf, "head_dim", None) or hf.hidden_size // hf.num_attention_heads
+        layers = hf.num_hidden_layers
+        block_bytes = 2 * layers * self.block_size * hf.num_key_value_heads * head_dim * kv_dtype.itemsize
+        if self.eagle3_model is not None:
+            ec = self.eagle3_model.config
+            block_bytes += 2 * self.block_size * ec.num_key_value_heads * ec.head_dim * ec.torch_dtype.itemsize
+        free, total = torch.cuda.mem_get_info(self.device)
+        used = total - free
+        stats = torch.cuda.memory_stats(self.device)
+        peak = stats["allocated_bytes.all.peak"]
+        current = stats["allocated_bytes.all.current"]
+        budget = int(total * config.gpu_memory_utilization - used - peak + current)
+        num_blocks = budget // block_bytes
+        if config.num_kvcache_blocks > 0:
+            num_blocks = min(num_blocks, config.num_kvcache_blocks)
+        if num_blocks <= 0:
+            raise RuntimeError("not enough GPU memory for the KV cache")
+        config.num_kvcache_blocks = int(num_blocks)
+        self.kv_cache = torch.empty(2, layers, num_blocks, self.block_size,
+                                    hf.num_key_value_heads, head_dim, dtype=kv_dtype,
+                                    device=self.device)
+        attns = [m for m in self.model.modules() if isinstance(m, Attention)]
+        assert len(attns) == layers
+        for i, m in enumerate(attns):
+            m.k_cache = self.kv_cache[0, i]
+            m.v_cache = self.kv_cache[1, i]
+        self.eagle_kv_cache = None
+        if self.eagle3_model is not None:
+            # same block ids as the target: the scheduler's block table and its
+            # logical rollback govern both caches
+            ec = self.eagle3_model.config
+            d_attns = [m for m in self.eagle3_model.modules() if isinstance(m, Attention)]
+            self.eagle_kv_cache = torch.empty(2, len(d_attns), num_blocks, self.block_size,
+                                              ec.num_key_value_heads, ec.head_dim,
+                                              dtype=ec.torch_dtype, device=self.device)
+            for i, m in enumerate(d_attns):
+                m.k_cache = self.eagle_kv_cache[0, i]
+                m.v_cache = self.eagle_kv_cache[1, i]
+
+    # ------------------------------------------------------------ metadata
+
+    def _slot(self, seq: Sequence, position: int) -> int:
+        return seq.block_table[position // self.block_size] * self.block_size + position % self.block_size
+
+    def prepare_block_tables(self, seqs: list[Sequence]) -> torch.Tensor:
+        width = max(len(seq.block_table) for seq in seqs)
+        rows = [seq.block_table + [-1] * (width - len(seq.block_table)) for seq in seqs]
+        return _pinned(rows, torch.int32).to(self.device, non_blocking=True)
+
+    def prepare_prefill(self, seqs: list[Sequence]):
+        """Varlen metadata for rows [num_computed, num_computed + scheduled)
+        of each sequence (model_runner.py:761-800).  Also used by verify."""
+        input_ids, positions, slots = [], [], []
+        cu_q, cu_k = [0], [0]
+        max_q = max_k = 0
+        for seq in seqs:
+            start = seq.num_computed_tokens
+            scheduled = seq.num_scheduled_tokens or seq.num_tokens
+            end = min(start + scheduled, seq.num_tokens)
+            input_ids.extend(seq.token_ids[start:end])
+            positions.extend(range(start, end))
+            cu_q.append(cu_q[-1] + end - start)
+            cu_k.append(cu_k[-1] + end)
+            max_q = max(max_q, end - start)
+            max_k = max(max_k, end)
+            if seq.block_table:
+                slots.extend(self._slot(seq, p) for p in range(start, end))
+        block_tables = None
+        if any(seq.block_table for seq in seqs):
+            if not all(seq.block_table for seq in seqs):
+                raise RuntimeError("mixed allocated and unallocated KV-cache batches")
+            block_tables = self.prepare_block_tables(seqs)
+        dev = self.device
+        ids_t = _pinned(input_ids, torch.int64).to(dev, non_blocking=True)
+        pos_t = _pinned(positions, torch.int64).to(dev, non_blocking=True)
+        set_context(True, _pinned(cu_q, torch.int32).to(dev, non_blocking=True),
+                    _pinned(cu_k, torch.int32).to(dev, non_blocking=True), max_q, max_k,
+                    _pinned(slots, torch.int32).to(dev, non_blocking=True), None, block_tables)
+        self._host_prefill = (input_ids, cu_q)
+        return ids_t, pos_t
+
+    def prepare_decode(self, seqs: list[Sequence]):
+        """One row per sequence at its last token (model_runner.py:802-836)."""
+        input_ids = [seq.last_token for seq in seqs]
+        positions = [len(seq) - 1 for seq in seqs]
+        context_lens = [len(seq) for seq in seqs]
+        slots = [seq.block_table[-1] * self.block_size + seq.last_block_num_tokens - 1
+                 for seq in seqs]
+        dev = self.device
+        cu_q = list(range(len(seqs) + 1))
+        cu_k = [0]
+        for n in context_lens:
+            cu_k.append(cu_k[-1] + n)
+        set_context(False, _pinned(cu_q, torch.int32).to(dev, non_blocking=True),
+                    _pinned(cu_k, torch.int32).to(dev, non_blocking=True), 1, max(context_lens),
+                    _pinned(slots, torch.int32).to(dev, non_blocking=True),
+                    _pinned(context_lens, torch.int32).to(dev, non_blocking=True),
+                    self.prepare_block_tables(seqs))
+        return (_pinned(input_ids, torch.int64).to(dev, non_blocking=True),
+                _pinned(positions, torch.int64).to(dev, non_blocking=True))
+
+    def prepare_sample(self, seqs: list[Sequence]) -> torch.Tensor:
+        return _pinned([seq.temperature for seq in seqs], torch.float32).to(self.device,
+                                                                             non_blocking=True)
+
+    # ------------------------------------------------------------ sampling
+
+    def sample(self, logits: torch.Tensor, temperatures: torch.Tensor) -> torch.Tensor:
+        """Greedy rows use the argmax kernel; temperature rows the
+        exponential-race sampler of layers/sampler.py:10-19."""
+        greedy = K.argmax_rows(logits)
+        if not bool((temperatures > 0).any()):
+            return greedy
+        probs = torch.softmax(logits.float() / temperatures.clamp_min(1e-10).unsqueeze(1), dim=-1)
+        sampled = probs.div_(torch.empty_like(probs).exponential_(1).clamp_min_(1e-10)).argmax(-1)
+        return torch.where(temperatures == 0, greedy, sampled)
+
+    # ------------------------------------------------------------ plain steps
+
+    @torch.inference_mode()
+    def run(self, seqs: list[Sequence], is_prefill: bool) -> list[int]:
+        if not seqs:
+            raise ValueError("empty batch")
+        try:
+            if is_prefill:
+                input_ids, positions = self.prepare_prefill(seqs)
+            else:
+                if self.speculative_config is not None:
+                    raise RuntimeError("EAGLE3 target runner received an unsupported decode")
+                input_ids, positions = self.prepare_decode(seqs)
+            temperatures = self.prepare_sample(seqs)
+            if self.speculative_config is not None:
+                return self._run_prefill_eagle3(seqs, input_ids, positions, temperatures)
+            hidden = self.model(input_ids, positions)
+            if is_prefill:
+                last = get_context().cu_seqlens_q[1:].long() - 1
+                hidden = hidden[last]
+            logits = self.model.compute_logits(hidden)
+            return self.sample(logits, temperatures).tolist()
+        finally:
+            reset_context()
+
+    def _run_prefill_eagle3(self, seqs, input_ids, positions, temperatures) -> list[int]:
+        """Target prefill with aux states, then the draft over the same rows
+        (its K/V at the same slots) to seed each sequence's recurrent state
+        (model_runner.py:1020-1044, :1369-1391)."""
+        ctx = get_context()
+        hidden, aux = self.model.forward_with_aux_hidden_states(
+            input_ids, positions, self.speculative_config.aux_hidden_state_layers)
+        last = ctx.cu_seqlens_q[1:].long() - 1
+        next_tokens = self.sample(self.model.compute_logits(hidden[last]), temperatures)
+        host_ids, cu = self._host_prefill
+        # draft input at row p is token p+1; the last row takes the sampled
+        # token (or the next prompt token when the prompt continues)
+        shifted = list(host_ids[1:]) + [0]
+        next_host = next_tokens.tolist()
+        for i, seq in enumerate(seqs):
+            end_pos = seq.num_computed_tokens + (cu[i + 1] - cu[i])
+            shifted[cu[i + 1] - 1] = (next_host[i] if end_pos >= seq.num_tokens
+                                      else seq.token_ids[end_pos])
+        eagle_ids = _pinned(shifted, torch.int64).to(self.device, non_blocking=True)
+        combined = self.eagle3_model.combine_hidden_states(aux_concat(aux))
+        d_hidden, d_feedback = self.eagle3_model.forward_with_cache(eagle_ids, positions, combined)
+        for i, seq in enumerate(seqs):
+            r = cu[i + 1] - 1
+            self.eagle3_states[seq.seq_id] = Eagle3KVCache(d_hidden[r:r + 1].clone(),
+                                                           d_feedback[r:r + 1].clone())
+        return next_host
+
+    # ------------------------------------------------------------ EAGLE3
+
+    def get_eagle3_runtime_capabilities(self):
+        return {
+            "paged_kv_cache": bool(getattr(self, "eagle3_model", None) is not None
+                                   and getattr(self, "eagle_kv_cache", None) is not None),
+            "cuda_graph": bool(getattr(self, "eagle_graphs", {})),
+            "graph_batch_sizes": sorted(getattr(self, "eagle_graphs", {})),
+        }
+
+    @torch.inference_mode()
+    def propose_eagle3_batch(self, seqs: list[Sequence]) -> list[list[int]]:
+        """k greedy draft tokens per sequence (fewer near max_tokens) from the
+        recurrent states (model_runner.py:1159-1213).  Metadata for every
+        step goes to the device in one copy; the proposals come back in one."""
+        assert self.eagle3_model is not None
+        k = self.speculative_config.num_speculative_tokens
+        limits = [min(k, seq.max_tokens - seq.num_completion_tokens) for seq in seqs]
+        steps = max(limits, default=0)
+        if steps <= 0:
+            return [[] for _ in seqs]
+        try:
+            hidden = torch.cat([self.eagle3_states[s.seq_id].last_hidden_state for s in seqs])
+            feedback = torch.cat([self.eagle3_states[s.seq_id].last_feedback_hidden_state
+                                  for s in seqs])
+            tokens = [self.eagle3_model.sample_greedy(hidden)]
+            if steps > 1:
+                lens = [len(seq) for seq in seqs]
+                pos = [[n - 1 + s for n in lens] for s in range(steps - 1)]
+                slots = [[self._slot(seq, p) for seq, p in zip(seqs, row)] for row in pos]
+                ctx_lens = [[p + 1 for p in row] for row in pos]
+                pos_d = _pinned(pos, torch.int64).to(self.device, non_blocking=True)
+                slot_d = _pinned(slots, torch.int32).to(self.device, non_blocking=True)
+                ctx_d = _pinned(ctx_lens, torch.int32).to(self.device, non_blocking=True)
+                block_tables = self.prepare_block_tables(seqs)
+                for s in range(steps - 1):
+                    set_context(False, slot_mapping=slot_d[s], context_lens=ctx_d[s],
+                                block_tables=block_tables, max_seqlen_k=max(lens) + s)
+                    hidden, feedback = self.eagle3_model.forward_with_cache(tokens[-1], pos_d[s],
+                                                                            feedback)
+                    tokens.append(self.eagle3_model.sample_greedy(hidden))
+            table = torch.stack(tokens).cpu().tolist()
+            return [[table[s][i] for s in range(limits[i])] for i in range(len(seqs))]
+        finally:
+            reset_context()
+
+    @torch.inference_mode()
+    def verify_eagle3_batch_fused(self, seqs: list[Sequence], num_input_tokens: list[int]):
+        """Target forward over [previous token, drafts] of every sequence, then
+        the fused argmax + accept kernel.  Returns host lists
+        (target_tokens per sequence, accept_len, bonus); the aux hidden-state
+        pairs stay on the device for ``commit_eagle3_batch``."""
+        if len(seqs) != len(num_input_tokens):
+            raise ValueError("EAGLE3 verification metadata does not match requests")
+        try:
+            for seq, n in zip(seqs, num_input_tokens):
+                seq.num_scheduled_tokens = n
+            input_ids, positions = self.prepare_prefill(seqs)
+            ctx = get_context()
+            hidden, aux = self.model.forward_with_aux_hidden_states(
+                input_ids, positions, self.speculative_config.aux_hidden_state_layers)
+            logits = self.model.compute_all_logits(hidden)
+            t, b = logits.shape[0], len(seqs)
+            n = t + 2 * b
+            if n > self._verify_dev.numel():
+                self._verify_dev = torch.empty(2 * n, dtype=torch.int32, device=self.device)
+                self._verify_host = torch.empty(2 * n, dtype=torch.int32, pin_memory=True)
+            K.argmax_accept(logits, ctx.cu_seqlens_q, input_ids, out=self._verify_dev[:n])
+            self._verify_host[:n].copy_(self._verify_dev[:n], non_blocking=True)
+            torch.cuda.current_stream().synchronize()
+            res = self._verify_host[:n].tolist()
+            _, cu = self._host_prefill
+            if self.keep_verify_inputs:
+                self.last_verify_inputs = (logits, list(cu), input_ids)
+            argmax = res[:t]
+            targets = [argmax[cu[i]:cu[i + 1]] for i in range(b)]
+            self._pending_verify = (aux, cu, {seq.seq_id: i for i, seq in enumerate(seqs)})
+            return targets, res[t:t + b], res[t + b:n]
+        finally:
+            for seq in seqs:
+                seq.num_scheduled_tokens = 0
+            reset_context()
+
+    @torch.inference_mode()
+    def verify_eagle3_batch(self, seqs: list[Sequence], num_input_tokens: list[int]):
+        """Reference-shaped result (model_runner.py:1047-1078): per-sequence
+        target argmax lists and aux hidden-state rows [q_i, 3H]."""
+        targets, _, _ = self.verify_eagle3_batch_fused(seqs, num_input_tokens)
+        aux, cu, _ = self._pending_verify
+        full = aux_concat(aux)
+        return targets, [full[cu[i]:cu[i + 1]] for i in range(len(seqs))]
+
+    @torch.inference_mode()
+    def commit_eagle3_batch(self, seqs: list[Sequence], output_tokens: list[list[int]],
+                            start_positions: list[int]) -> None:
+        """Replay every sequence's committed tail into the draft cache in one
+        ragged forward.  Sequence i's verify rows cu[i] .. cu[i] + n_i - 1 hold
+        the aux states of positions start_i .. start_i + n_i - 1, paired with
+        its committed tokens (model_runner.py:1216-1249 does this one token
+        and one sequence at a time)."""
+        if self._pending_verify is None:
+            raise RuntimeError("commit_eagle3_batch needs a preceding verify")
+        aux, cu, index = self._pending_verify
+        rows = []
+        for seq, toks in zip(seqs, output_tokens):
+            i = index[seq.seq_id]
+            if len(toks) > cu[i + 1] - cu[i]:
+                raise RuntimeError("committed tail longer than the verify window")
+            rows.extend(range(cu[i], cu[i] + len(toks)))
+        if not rows:
+            return
+        rows_d = _pinned(rows, torch.int32).to(self.device, non_blocking=True)
+        combined = self.eagle3_model.combine_hidden_states(aux_concat(aux, rows_d))
+        self._draft_commit(seqs, output_tokens, start_positions, combined)
+
+    @torch.inference_mode()
+    def commit_eagle3(self, seq: Sequence, output_tokens: list[int],
+                      target_aux_hidden_states: torch.Tensor, start_position: int) -> None:
+        """Single-sequence form of the reference (model_runner.py:1216-1249)."""
+        if not output_tokens or seq.is_finished:
+            return
+        combined = self.eagle3_model.combine_hidden_states(
+            target_aux_hidden_states[:len(output_tokens)])
+        self._draft_commit([seq], [output_tokens], [start_position], combined)
+
+    def _draft_commit(self, seqs, output_tokens, start_positions, combined) -> None:
+        ids, pos, slots = [], [], []
+        cu_q, cu_k = [0], [0]
+        for seq, toks, start in zip(seqs, output_tokens, start_positions):
+            n = len(toks)
+            ids.extend(toks)
+            pos.extend(range(start, start + n))
+            slots.extend(self._slot(seq, p) for p in range(start, start + n))
+            cu_q.append(cu_q[-1] + n)
+            cu_k.append(cu_k[-1] + start + n)
+        dev = self.device
+        try:
+            set_context(True, _pinned(cu_q, torch.int32).to(dev, non_blocking=True),
+                        _pinned(cu_k, torch.int32).to(dev, non_blocking=True),
+                        max(len(t) for t in output_tokens),
+                        max(s + len(t) for s, t in zip(start_positions, output_tokens)),
+                        _pinned(slots, torch.int32).to(dev, non_blocking=True), None,
+                        self.prepare_block_tables(seqs))
+            hidden, feedback = self.eagle3_model.forward_with_cache(
+                _pinned(ids, torch.int64).to(dev, non_blocking=True),
+                _pinned(pos, torch.int64).to(dev, non_blocking=True), combined)
+            for i, seq in enumerate(seqs):
+                r = cu_q[i + 1] - 1
+                self.eagle3_states[seq.seq_id] = Eagle3KVCache(hidden[r:r + 1].clone(),
+                                                               feedback[r:r + 1].clone())
+        finally:
+            reset_context()
+
+    def release_eagle3_state(self, seq_id: int) -> None:
+        self.eagle3_states.pop(seq_id, None)
+
+    @torch.inference_mode()
+    def run_eagle3_graph(self, input_ids, positions, feedback, seqs):
+        """Replay the captured draft step of the smallest batch bucket >= len(seqs)
+        after copying inputs and the current paged metadata into its static
+        buffers (model_runner.py:1526-1548)."""
+        bs = len(seqs)
+        graph_bs = next(size for size in sorted(self.eagle_graphs) if size >= bs)
+        graph = self.eagle_graphs[graph_bs]
+        v = self.eagle_graph_vars[graph_bs]
+        v["input_ids"].zero_()
+        v["positions"].zero_()
+        v["feedback"].zero_()
+        v["slot_mapping"].fill_(-1)
+        v["context_lens"].fill_(1)
+        v["block_tables"].zero_()
+        v["input_ids"][:bs].copy_(input_ids)
+        v["positions"][:bs].copy_(positions)
+        v["feedback"][:bs].copy_(feedback)
+        ctx = get_context()
+        v["slot_mapping"][:bs].copy_(ctx.slot_mapping)
+        v["context_lens"][:bs].copy_(ctx.context_lens)
+        v["block_tables"][:bs, :ctx.block_tables.size(1)].copy_(ctx.block_tables)
+        graph.replay()
+        hidden, next_feedback = v["outputs"]
+        return hidden[:bs], next_feedback[:bs]
+
+    # ------------------------------------------------------------ diagnostics
+
+    def get_diagnostics(self):
+        return {
+            "device": str(self.device),
+            "parameter_bytes": param_bytes(self.model),
+            "draft_parameter_bytes": param_bytes(self.eagle3_model) if self.eagle3_model else 0,
+            "kv_cache_dtype": str(self.kv_cache.dtype),
+            "kv_cache_blocks": self.kv_cache.size(2),
+            "kv_cache_bytes": self.kv_cache.numel() * self.kv_cache.element_size(),
+            "decode_graph_replay_count": self.decode_graph_replay_count,
+            "eagle3_runtime": self.get_eagle3_runtime_capabilities(),
+        }

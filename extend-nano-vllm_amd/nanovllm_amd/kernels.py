@@ -71,8 +71,7 @@ class _Workspaces:
     """Per-(device, kind) scratch buffers that only grow.
 
     Superseded buffers are kept alive because captured graphs may still point
-    at them.  'argmax' buffers are zero-filled on allocation; the kernels keep
-    them zero-filled."""
+    at them."""
 
     def __init__(self) -> None:
         self._bufs: dict[tuple[int, str], torch.Tensor] = {}
@@ -107,9 +106,9 @@ def argmax_workspace_bytes(num_rows: int, num_seqs: int, vocab: int) -> int:
 
 
 def attention_workspace_bytes(num_seqs: int, num_tokens: int, num_q_heads: int, num_kv_heads: int,
-                              head_dim: int, max_seqlen_k: int) -> int:
+                              head_dim: int, max_seqlen_q: int, max_seqlen_k: int) -> int:
     return int(_native.load().nva_paged_attention_workspace_size(
-        num_seqs, num_tokens, num_q_heads, num_kv_heads, head_dim, max_seqlen_k))
+        num_seqs, num_tokens, num_q_heads, num_kv_heads, head_dim, max_seqlen_q, max_seqlen_k))
 
 
 # ---------------------------------------------------------------- K2
@@ -338,7 +337,7 @@ def paged_attention_varlen(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     if cu_seqlens_k.numel() != b + 1 or block_table.shape[0] < b:
         raise ValueError("cu_seqlens_k / block_table do not match cu_seqlens_q")
     out = _q_out(q, out)
-    nbytes = attention_workspace_bytes(b, t, hq, hkv, d, max_seqlen_k)
+    nbytes = attention_workspace_bytes(b, t, hq, hkv, d, max_seqlen_q, max_seqlen_k)
     ws = _WS.get(q.device, "attention", nbytes) if nbytes else None
     check(lib.nva_paged_attention_varlen(
         q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), kvd, bstr,
@@ -379,7 +378,7 @@ def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     if max_seqlen_k is None:
         max_seqlen_k = block_table.shape[1] * bs
     out = _q_out(q, out)
-    nbytes = attention_workspace_bytes(b, b, hq, hkv, d, max_seqlen_k)
+    nbytes = attention_workspace_bytes(b, b, hq, hkv, d, 1, max_seqlen_k)
     ws = _WS.get(q.device, "attention", nbytes) if nbytes else None
     check(lib.nva_paged_attention_decode(
         q.data_ptr(), q.stride(0), q.stride(1), k_cache.data_ptr(), v_cache.data_ptr(), kvd, bstr,
@@ -404,3 +403,76 @@ def fp8_paged_decode_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: 
         raise ValueError("num query heads must divide evenly by KV heads")
     return paged_attention_decode(q, k_cache, v_cache, context_lens, block_tables, scale,
                                   k_scale=k_scale, v_scale=v_scale)
+
+
+# ---------------------------------------------------------------- forward helpers
+
+def _rows2d(x: torch.Tensor, name: str) -> None:
+    if x.dtype != BF16 or x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError(f"{name} must be bf16 [rows, hidden] with unit last stride")
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+             out: torch.Tensor | None = None) -> torch.Tensor:
+    """RMSNorm without residual (layers/layernorm.py:70-89)."""
+    lib = _native.load()
+    _require_cuda(x, weight, out)
+    _rows2d(x, "x")
+    rows, h = x.shape
+    if out is None:
+        out = torch.empty(rows, h, dtype=BF16, device=x.device)
+    check(lib.nva_rms_norm(x.data_ptr(), x.stride(0), weight.data_ptr(), out.data_ptr(),
+                           out.stride(0), rows, h, float(eps), _stream()), "rms_norm")
+    return out
+
+
+def add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float):
+    """RMSNorm with residual add (layers/layernorm.py:91-107).
+
+    Returns (normed, new_residual); both are new tensors."""
+    lib = _native.load()
+    _require_cuda(x, residual, weight)
+    _rows2d(x, "x")
+    _rows2d(residual, "residual")
+    rows, h = x.shape
+    out = torch.empty(rows, h, dtype=BF16, device=x.device)
+    res_out = torch.empty(rows, h, dtype=BF16, device=x.device)
+    check(lib.nva_add_rms_norm(x.data_ptr(), x.stride(0), residual.data_ptr(), residual.stride(0),
+                               weight.data_ptr(), out.data_ptr(), out.stride(0), res_out.data_ptr(),
+                               res_out.stride(0), rows, h, float(eps), _stream()), "add_rms_norm")
+    return out, res_out
+
+
+def qk_norm_rope(qkv: torch.Tensor, positions: torch.Tensor, q_norm_weight: torch.Tensor | None,
+                 k_norm_weight: torch.Tensor | None, cos_sin: torch.Tensor, num_q_heads: int,
+                 num_kv_heads: int, head_dim: int, eps: float):
+    """Per-head q/k RMSNorm + neox RoPE on a fused QKV output
+    (models/qwen3.py:77-98).  Returns contiguous q [T, Hq, D], k [T, Hkv, D]."""
+    lib = _native.load()
+    _require_cuda(qkv, positions, q_norm_weight, k_norm_weight, cos_sin)
+    _rows2d(qkv, "qkv")
+    if positions.dtype != torch.int64 or not positions.is_contiguous():
+        raise TypeError("positions must be contiguous int64")
+    if cos_sin.dtype != torch.float32 or not cos_sin.is_contiguous():
+        raise TypeError("cos_sin must be contiguous float32 [max_position, head_dim]")
+    t = qkv.shape[0]
+    q = torch.empty(t, num_q_heads, head_dim, dtype=BF16, device=qkv.device)
+    k = torch.empty(t, num_kv_heads, head_dim, dtype=BF16, device=qkv.device)
+    check(lib.nva_qk_norm_rope(qkv.data_ptr(), qkv.stride(0), positions.data_ptr(),
+                               _ptr(q_norm_weight), _ptr(k_norm_weight), cos_sin.data_ptr(),
+                               cos_sin.shape[0], t, num_q_heads, num_kv_heads, head_dim,
+                               float(eps), q.data_ptr(), k.data_ptr(), _stream()), "qk_norm_rope")
+    return q, k
+
+
+def silu_mul(x: torch.Tensor) -> torch.Tensor:
+    """SiluAndMul (layers/activation.py:11-14) on rows [a | b]."""
+    lib = _native.load()
+    _require_cuda(x)
+    _rows2d(x, "x")
+    rows, two_i = x.shape
+    inter = two_i // 2
+    out = torch.empty(rows, inter, dtype=BF16, device=x.device)
+    check(lib.nva_silu_mul(x.data_ptr(), x.stride(0), out.data_ptr(), out.stride(0), rows, inter,
+                           _stream()), "silu_mul")
+    return out

@@ -127,8 +127,8 @@ int nva_aux_gather(const void *const *hidden, const void *const *residual, int32
  *   argmax[row accept_len] (the replacement or bonus token).  A sequence with
  *   q_i == 0 gets accept_len 0 and bonus -1.
  * workspace: nva_argmax_workspace_size(num_tokens, num_seqs, vocab) bytes,
- *   ZERO-FILLED by the caller before its first use; every call leaves it
- *   zero-filled again (its counters reset themselves).
+ *   8-byte aligned, no initialisation needed (per-chunk partial maxima).
+ * Two kernels are enqueued (chunk partials, then a per-sequence merge).
  * ------------------------------------------------------------------- */
 size_t nva_argmax_workspace_size(int32_t num_rows, int32_t num_seqs, int32_t vocab);
 
@@ -172,8 +172,8 @@ int nva_argmax_rows(const void *logits, int64_t row_stride, int32_t vocab, int32
  *      multiplied by *k_scale and the output by *v_scale (NULL = 1.0), as in
  *      the reference's FP8 decode kernel; bf16 caches ignore the scales.
  *   GQA: query head h reads kv head h / (num_q_heads / num_kv_heads).
- *   head_dim must be 128 and block_size a multiple of 32;
- *      max_seqlen_q * (num_q_heads / num_kv_heads) must be <= 64.
+ *   head_dim must be 128, block_size a multiple of 32 and
+ *      num_q_heads / num_kv_heads <= 64; any query length is accepted.
  *   workspace: nva_paged_attention_workspace_size(...) bytes (split-KV
  *      partial results; needs no initialisation).
  * ------------------------------------------------------------------- */
@@ -188,7 +188,8 @@ int nva_argmax_rows(const void *logits, int64_t row_stride, int32_t vocab, int32
  *   L_i (they size the grid; larger device values are clipped to them). */
 size_t nva_paged_attention_workspace_size(int32_t num_seqs, int32_t num_tokens,
                                           int32_t num_q_heads, int32_t num_kv_heads,
-                                          int32_t head_dim, int32_t max_seqlen_k);
+                                          int32_t head_dim, int32_t max_seqlen_q,
+                                          int32_t max_seqlen_k);
 
 int nva_paged_attention_varlen(const void *q, int64_t q_row_stride, int64_t q_head_stride,
                                const void *k_cache, const void *v_cache, int kv_dtype,
@@ -221,6 +222,43 @@ int nva_paged_attention_decode(const void *q, int64_t q_row_stride, int64_t q_he
                                float softmax_scale, const float *k_scale, const float *v_scale,
                                void *out, int64_t out_row_stride, int64_t out_head_stride,
                                void *workspace, size_t workspace_bytes, void *stream);
+
+/* ---------------------------------------------------------------------
+ * Supporting per-token kernels of the target / draft forward (between the
+ * projection GEMMs, which stay on hipBLASLt through torch).  bf16 in/out,
+ * fp32 math; rounding follows the reference's eager formulas.
+ * ------------------------------------------------------------------- */
+
+/* RMSNorm.forward without residual (nanovllm/layers/layernorm.py:70-89):
+ *   out = bf16(bf16(x * rsqrt(mean(x^2) + eps)) * weight), per row. */
+int nva_rms_norm(const void *x, int64_t x_row_stride, const void *weight, void *out,
+                 int64_t out_row_stride, int32_t rows, int32_t hidden, float eps, void *stream);
+
+/* RMSNorm.forward with residual (add_rms_forward, layernorm.py:91-107):
+ *   s = f32(x) + f32(residual); residual_out = bf16(s);
+ *   out = bf16(bf16(s * rsqrt(mean(s^2) + eps)) * weight). */
+int nva_add_rms_norm(const void *x, int64_t x_row_stride, const void *residual,
+                     int64_t residual_row_stride, const void *weight, void *out,
+                     int64_t out_row_stride, void *residual_out, int64_t residual_out_row_stride,
+                     int32_t rows, int32_t hidden, float eps, void *stream);
+
+/* Qwen3Attention.project_qkv after the QKV GEMM (nanovllm/models/qwen3.py:
+ *   77-98): per-head q/k RMSNorm (skipped when both norm weights are NULL,
+ *   the EAGLE3 draft layer) then neox rotary embedding
+ *   (nanovllm/layers/rotary_embedding.py:6-48) with cos_sin a float32
+ *   [max_position, head_dim] table (cos | sin halves).  qkv rows hold
+ *   [q heads | k heads | v heads]; q_out [T, Hq, D] and k_out [T, Hkv, D] are
+ *   contiguous.  head_dim must be 128. */
+int nva_qk_norm_rope(const void *qkv, int64_t row_stride, const int64_t *positions,
+                     const void *q_norm_weight, const void *k_norm_weight, const float *cos_sin,
+                     int32_t max_position, int32_t num_tokens, int32_t num_q_heads,
+                     int32_t num_kv_heads, int32_t head_dim, float eps, void *q_out, void *k_out,
+                     void *stream);
+
+/* SiluAndMul (nanovllm/layers/activation.py:11-14): x rows [a | b] of
+ *   2*intermediate elements -> out = bf16(bf16(silu(a)) * b). */
+int nva_silu_mul(const void *x, int64_t x_row_stride, void *out, int64_t out_row_stride,
+                 int32_t rows, int32_t intermediate, void *stream);
 
 #ifdef __cplusplus
 }

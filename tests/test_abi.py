@@ -52,7 +52,7 @@ def test_host_side_argument_errors_without_gpu():
     # zero-size work is a no-op
     assert lib.nva_argmax_rows(None, 8, 8, 0, None, None, None, 0, None) == _native.NVA_OK
     assert lib.nva_argmax_workspace_size(384, 64, 151936) > 0
-    assert lib.nva_paged_attention_workspace_size(64, 384, 32, 8, 128, 2304) > 0
+    assert lib.nva_paged_attention_workspace_size(64, 384, 32, 8, 128, 6, 2304) > 0
     with pytest.raises(ValueError):
         _native.check(_native.NVA_ERR_ARG, "probe")
     with pytest.raises(_native.KernelError):

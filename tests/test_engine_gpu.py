@@ -1,0 +1,181 @@
+"""End-to-end EAGLE3 engine on the GPU with random-weight tiny models.
+
+The emitted tokens must be the target's greedy tokens: every generated token
+equals the argmax of the target's logits given the generated prefix
+(teacher-forced), except where the top-2 logit margin is below 2e-2, and the
+speculative and non-speculative engines agree up to such a near tie.
+Acceptance paths (accepted drafts, bonus tokens, page crossings, max_tokens
+clipping) are exercised with proposals taken from the target's own greedy
+continuation, partly corrupted.
+"""
+import pytest
+import torch
+
+from nanovllm_amd import LLM, SamplingParams
+from nanovllm_amd.engine.sequence import Sequence
+from nanovllm_amd.synthetic import write_eagle3_config, write_qwen3_config
+
+pytestmark = pytest.mark.gpu
+
+MARGIN_TOL = 2e-2
+AUX = (1, 2, 4)
+
+
+@pytest.fixture(scope="module")
+def dirs(tmp_path_factory):
+    root = tmp_path_factory.mktemp("ckpt")
+    target = write_qwen3_config(str(root / "target"), "tiny")
+    draft = write_eagle3_config(str(root / "draft"), "tiny", aux_layers=AUX)
+    return target, draft
+
+
+def make_llm(dirs, spec=True, k=4, blocks=96):
+    target, draft = dirs
+    kw = dict(load_format="dummy", seed=0, max_model_len=2048, num_kvcache_blocks=blocks,
+              enforce_eager=True, max_num_batched_tokens=4096)
+    if spec:
+        kw["speculative_config"] = {"method": "eagle3", "model": draft,
+                                    "num_speculative_tokens": k, "aux_hidden_state_layers": AUX}
+    return LLM(target, **kw)
+
+
+def prompts(n, seed=0, lo=5, hi=300):
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(lo, hi, (n,), generator=g).tolist()
+    return [torch.randint(0, 2048, (L,), generator=g).tolist() for L in lens]
+
+
+@torch.inference_mode()
+def teacher_forced_logits(llm, tokens):
+    """Target logits at every position of ``tokens`` (a fresh prefill)."""
+    runner = llm.model_runner
+    bm = llm.scheduler.block_manager
+    seq = Sequence(tokens)
+    bm.allocate(seq)
+    seq.num_computed_tokens = 0
+    seq.num_scheduled_tokens = len(tokens)
+    try:
+        ids, pos = runner.prepare_prefill([seq])
+        hidden = runner.model(ids, pos)
+        return runner.model.compute_all_logits(hidden).float().cpu()
+    finally:
+        from nanovllm_amd.context import reset_context
+        reset_context()
+        bm.deallocate(seq)
+
+
+def check_greedy(llm, prompt, out):
+    logits = teacher_forced_logits(llm, prompt + out)
+    full = prompt + out
+    bad = []
+    for p in range(len(prompt), len(full)):
+        row = logits[p - 1]
+        top2 = row.topk(2).values
+        if int(row.argmax()) != full[p] and float(top2[0] - top2[1]) >= MARGIN_TOL:
+            bad.append(p)
+    return bad
+
+
+def assert_same_greedy_path(llm, prompt, got, ref):
+    """``got`` is a valid greedy path of the target and equals ``ref`` up to
+    their first difference, which must sit at a near tie."""
+    assert len(got) == len(ref)
+    assert check_greedy(llm, prompt, got) == []
+    n = next((i for i, (x, y) in enumerate(zip(got, ref)) if x != y), None)
+    if n is not None:
+        row = teacher_forced_logits(llm, prompt + got[:n])[-1]
+        top2 = row.topk(2).values
+        assert float(top2[0] - top2[1]) < MARGIN_TOL, (n, float(top2[0] - top2[1]))
+
+
+def test_spec_equals_target_greedy(dirs):
+    ps = prompts(6, seed=1)
+    sp = SamplingParams(temperature=0.0, max_tokens=40, ignore_eos=True)
+    spec = make_llm(dirs, spec=True)
+    try:
+        outs = [o["token_ids"] for o in spec.generate(ps, sp, use_tqdm=False)]
+        assert all(len(o) == 40 for o in outs)
+        for p, o in zip(ps, outs):
+            assert check_greedy(spec, p, o) == []
+        assert spec.spec_stats["steps"] > 0
+        assert spec.model_runner.get_eagle3_runtime_capabilities()["paged_kv_cache"]
+    finally:
+        spec.exit()
+    plain = make_llm(dirs, spec=False)
+    try:
+        ref = [o["token_ids"] for o in plain.generate(ps, sp, use_tqdm=False)]
+        for p, a, b in zip(ps, outs, ref):
+            # identical up to the first near tie (then both are valid greedy paths)
+            n = next((i for i, (x, y) in enumerate(zip(a, b)) if x != y), None)
+            if n is not None:
+                row = teacher_forced_logits(plain, p + a[:n])[-1]
+                top2 = row.topk(2).values
+                assert float(top2[0] - top2[1]) < MARGIN_TOL
+    finally:
+        plain.exit()
+
+
+def test_acceptance_paths_with_oracle_drafts(dirs):
+    """Proposals = the target's own greedy continuation, corrupted at a few
+    positions: exercises accepted prefixes, bonus tokens, multi-token commits,
+    page crossings (prompts near 256) and max_tokens clipping."""
+    ps = [prompts(1, seed=7, lo=240, hi=250)[0], prompts(1, seed=8, lo=20, hi=30)[0],
+          prompts(1, seed=9, lo=500, hi=510)[0]]
+    max_tokens = [37, 23, 30]
+    plain = make_llm(dirs, spec=False)
+    try:
+        ref = [plain.generate([p], SamplingParams(temperature=0.0, max_tokens=m, ignore_eos=True),
+                              use_tqdm=False)[0]["token_ids"] for p, m in zip(ps, max_tokens)]
+    finally:
+        plain.exit()
+    spec = make_llm(dirs, spec=True, k=5)
+    runner = spec.model_runner
+    original = runner.propose_eagle3_batch
+    calls = {"n": 0}
+    full = {tuple(p): p + r for p, r in zip(ps, ref)}
+
+    def oracle_propose(seqs):
+        drafted = original(seqs)        # keeps the draft model's own K/V and state path
+        out = []
+        for seq, d in zip(seqs, drafted):
+            seqfull = full[tuple(seq.prompt_token_ids)]
+            want = seqfull[len(seq):len(seq) + len(d)]
+            want = want + d[len(want):]
+            calls["n"] += 1
+            if calls["n"] % 3 == 0 and len(want) > 2:
+                want = list(want)
+                want[2] = (want[2] + 1) % 2048     # reject from the third draft on
+            out.append(want)
+        return out
+
+    runner.propose_eagle3_batch = oracle_propose
+    try:
+        for p, m, r in zip(ps, max_tokens, ref):
+            spec.add_request(p, SamplingParams(temperature=0.0, max_tokens=m, ignore_eos=True))
+        outs = {}
+        while not spec.is_finished():
+            for seq_id, toks in spec.step()[0]:
+                outs[seq_id] = toks
+        got = [outs[i] for i in sorted(outs)]
+        for p, a, b in zip(ps, got, ref):
+            assert_same_greedy_path(spec, p, a, b)
+        stats = spec.spec_stats
+        assert stats["accepted"] > stats["steps"]          # multi-token commits happened
+        assert stats["committed"] == sum(max_tokens) - len(ps)   # first token comes from prefill
+    finally:
+        spec.exit()
+
+
+def test_errors_match_reference(dirs):
+    spec = make_llm(dirs, spec=True)
+    try:
+        with pytest.raises(ValueError):
+            spec.add_request([1, 2, 3], SamplingParams(temperature=0.7))
+        with pytest.raises(ValueError):
+            spec.add_request([], SamplingParams(temperature=0.0))
+        with pytest.raises(ValueError):
+            spec.add_request([1] * 2040, SamplingParams(temperature=0.0, max_tokens=64))
+        with pytest.raises(ValueError):
+            spec.add_request("text prompt", SamplingParams(temperature=0.0))
+    finally:
+        spec.exit()
