@@ -43,6 +43,10 @@ static_assert(kWaves * 16 * kAccPitch <= kWaves * kVStage, "merge tile must fit 
 constexpr int kTargetWorkgroups = 2048;
 constexpr int kMinSplit = 128;
 constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kRescaleSlack = 8.0f;   // log2 headroom before the running max moves
+
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+typedef __attribute__((ext_vector_type(2))) float f32x2_t;
 
 struct AttnParams {
   const uint16_t* q;
@@ -71,6 +75,11 @@ struct AttnParams {
 };
 
 __device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Orders a wave's own LDS writes and reads: LDS executes one wave's
+// operations in issue order, so the compiler must only keep program order
+// and wait for outstanding LDS operations.
+__device__ __forceinline__ void lds_wave_sync() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
 __device__ __forceinline__ f32x4_t mfma(bf16x8_t a, bf16x8_t b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -120,7 +129,7 @@ paged_attention_kernel(AttnParams p) {
   const int qt = blockIdx.x / p.max_splits;
   const int kvh = blockIdx.y;
   const int seq = blockIdx.z;
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
   const int lane = threadIdx.x & (kWave - 1);
   const int g = lane >> 4;
   const int m16 = lane & 15;
@@ -192,19 +201,35 @@ paged_attention_kernel(AttnParams p) {
   uint32_t* vst = lds + wave * kVStage;
   const int nchunks = (kv_end - kv_begin + kChunk - 1) / kChunk;
   const int32_t* bt = p.block_tables + static_cast<int64_t>(seq) * p.bt_stride;
-  const int64_t esz = FP8 ? 1 : 2;
+  constexpr int64_t esz = FP8 ? 1 : 2;
 
-  for (int c = wave; c < nchunks; c += kWaves) {
-    const int kb = kv_begin + c * kChunk;
-    const int lblk = kb / p.block_size;
-    const int pblk = lblk < p.bt_cols ? bt[lblk] : -1;
-    if (pblk < 0 || pblk >= p.num_blocks) continue;   // empty block: keys masked
+  // Block ids of this split, one per lane (lane i holds logical block
+  // first_blk + i): one load up front instead of a dependent load per chunk.
+  const int first_blk = kv_begin / p.block_size;
+  const int nblk = (kv_end - 1) / p.block_size - first_blk + 1;
+  int lane_blk = -1;
+  if (lane < nblk && first_blk + lane < p.bt_cols) lane_blk = bt[first_blk + lane];
+  auto block_of = [&](int kb) -> int {
+    const int lb = kb / p.block_size;
+    const int rel = lb - first_blk;
+    int b;
+    if (rel < kWave)
+      b = __builtin_amdgcn_readlane(lane_blk, rel);
+    else
+      b = lb < p.bt_cols ? bt[lb] : -1;
+    return (b >= 0 && b < p.num_blocks) ? b : -1;   // invalid block: keys masked
+  };
+
+  // Raw K / V registers of one 32-key chunk.  K: lane holds key (16*kt + m16),
+  // head_dim elements 32*s + 8*g .. +7; V: coalesced rows for the LDS stage.
+  struct Chunk {
+    uint4 k[2][4];     // fp8 uses .x/.y only
+    uint4 v[8];        // fp8 uses v[0..3]
+  };
+  auto load = [&](int kb, int pblk, Chunk& r) {
     const int off0 = kb % p.block_size;
     const int64_t blk_base = static_cast<int64_t>(pblk) * p.blk_stride +
                              static_cast<int64_t>(kvh) * p.head_stride;
-
-    // ---- K operands: key (16*kt + m16), d slice s
-    bf16x8_t kop[2][4];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
       int key = kb + kt * 16 + m16;
@@ -214,53 +239,71 @@ paged_attention_kernel(AttnParams p) {
       for (int s = 0; s < 4; ++s) {
         if (FP8) {
           const uint2 w = *reinterpret_cast<const uint2*>(p.k_cache + (e + 32 * s + 8 * g));
-          kop[kt][s] = fp8x8_to_bf16(w);
+          r.k[kt][s] = make_uint4(w.x, w.y, 0, 0);
         } else {
-          kop[kt][s] = *reinterpret_cast<const bf16x8_t*>(p.k_cache + (e + 32 * s + 8 * g) * esz);
+          r.k[kt][s] = *reinterpret_cast<const uint4*>(p.k_cache + (e + 32 * s + 8 * g) * esz);
         }
       }
     }
-    // ---- V rows (coalesced) into the wave's LDS stage
     if (FP8) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int r = 8 * i + (lane >> 3);
-        int key = kb + r;
+        int key = kb + 8 * i + (lane >> 3);
         key = key < kv_limit ? key : kv_limit - 1;
         const int64_t e = blk_base + static_cast<int64_t>(off0 + key - kb) * p.tok_stride + (lane & 7) * 16;
-        const uint4 w = *reinterpret_cast<const uint4*>(p.v_cache + e);
-        const bf16x8_t a = fp8x8_to_bf16(make_uint2(w.x, w.y));
-        const bf16x8_t b = fp8x8_to_bf16(make_uint2(w.z, w.w));
-        uint32_t* dst = vst + r * kVPitch + (lane & 7) * 8;
-        *reinterpret_cast<bf16x8_t*>(dst) = a;
-        *reinterpret_cast<bf16x8_t*>(dst + 4) = b;
+        r.v[i] = *reinterpret_cast<const uint4*>(p.v_cache + e);
       }
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const int r = 4 * i + g;
-        int key = kb + r;
+        int key = kb + 4 * i + g;
         key = key < kv_limit ? key : kv_limit - 1;
         const int64_t e = blk_base + static_cast<int64_t>(off0 + key - kb) * p.tok_stride + m16 * 8;
-        const uint4 w = *reinterpret_cast<const uint4*>(p.v_cache + e * 2);
-        *reinterpret_cast<uint4*>(vst + r * kVPitch + m16 * 4) = w;
+        r.v[i] = *reinterpret_cast<const uint4*>(p.v_cache + e * esz);
       }
+    }
+  };
+
+  auto process = [&](int kb, const Chunk& r) {
+    // ---- V rows into the wave's LDS stage
+    if (FP8) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = 8 * i + (lane >> 3);
+        uint32_t* dst = vst + row * kVPitch + (lane & 7) * 8;
+        *reinterpret_cast<bf16x8_t*>(dst) = fp8x8_to_bf16(make_uint2(r.v[i].x, r.v[i].y));
+        *reinterpret_cast<bf16x8_t*>(dst + 4) = fp8x8_to_bf16(make_uint2(r.v[i].z, r.v[i].w));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i)
+        *reinterpret_cast<uint4*>(vst + (4 * i + g) * kVPitch + m16 * 4) = r.v[i];
     }
 
     // ---- S^T = K . Q^T
     f32x4_t sacc[2][NT];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
+      bf16x8_t kop[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+        kop[s] = FP8 ? fp8x8_to_bf16(make_uint2(r.k[kt][s].x, r.k[kt][s].y))
+                     : __builtin_bit_cast(bf16x8_t, r.k[kt][s]);
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         f32x4_t a = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 0; s < 4; ++s) a = mfma(kop[kt][s], qop[nt][s], a);
+        for (int s = 0; s < 4; ++s) a = mfma(kop[s], qop[nt][s], a);
         sacc[kt][nt] = a;
       }
     }
 
-    // ---- online softmax (per query column; lanes l, l^16, l^32, l^48 share one)
+    // ---- online softmax (per query column; lanes l, l^16, l^32, l^48 share one).
+    // Scores stay raw (the scale is folded into the exp2 argument); the
+    // running max m_run (scaled, log2 domain) is only raised when a column's
+    // new max exceeds it by more than kRescaleSlack, so the accumulator
+    // rescale is skipped for most chunks: probabilities stay <= 2^kRescaleSlack.
+    const bool full = kb + kChunk - 1 <= L - q_len + j0 && kb + kChunk <= kv_limit;
     bf16x8_t pb[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
@@ -270,41 +313,48 @@ paged_attention_kernel(AttnParams p) {
       for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int key = kb + kt * 16 + 4 * g + i;
-          float v = sacc[kt][nt][i] * sl2;
-          v = key <= lim[nt] ? v : -INFINITY;
+          float v = sacc[kt][nt][i];
+          if (!full) v = (kb + kt * 16 + 4 * g + i <= lim[nt]) ? v : -INFINITY;
           sv[kt * 4 + i] = v;
           cmax = fmaxf(cmax, v);
         }
       }
       cmax = fmaxf(cmax, __shfl_xor(cmax, 16, kWave));
       cmax = fmaxf(cmax, __shfl_xor(cmax, 32, kWave));
-      const float m_new = fmaxf(m_run[nt], cmax);
-      const float msub = m_new == -INFINITY ? 0.0f : m_new;
-      const float alpha = exp2f_fast(m_run[nt] - msub);
+      cmax *= sl2;
+      const bool need = cmax > m_run[nt] + kRescaleSlack;
+      if (__any(need)) {
+        const float m_new = need ? cmax : m_run[nt];
+        const float alpha = need ? exp2f_fast(m_run[nt] - m_new) : 1.0f;
+        l_run[nt] *= alpha;
+        m_run[nt] = m_new;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[nt][t][i] *= alpha;
+        }
+      }
+      const float msub = m_run[nt] == -INFINITY ? 0.0f : m_run[nt];
       float psum = 0.0f;
-      float pv[8];
+      f32x2_t pv[4];
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
-        pv[k] = exp2f_fast(sv[k] - msub);
-        psum += pv[k];
+        const float e = exp2f_fast(__builtin_fmaf(sv[k], sl2, -msub));
+        pv[k >> 1][k & 1] = e;
+        psum += e;
       }
-      l_run[nt] = l_run[nt] * alpha + psum;
-      m_run[nt] = m_new;
-#pragma unroll
-      for (int t = 0; t < 8; ++t) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[nt][t][i] *= alpha;
-      }
-      uint4 pk = make_uint4(pack_bf16(pv[0], pv[1]), pack_bf16(pv[2], pv[3]),
-                            pack_bf16(pv[4], pv[5]), pack_bf16(pv[6], pv[7]));
+      l_run[nt] += psum;
+      uint4 pk;
+      pk.x = __builtin_bit_cast(uint32_t, __builtin_convertvector(pv[0], bf16x2_t));
+      pk.y = __builtin_bit_cast(uint32_t, __builtin_convertvector(pv[1], bf16x2_t));
+      pk.z = __builtin_bit_cast(uint32_t, __builtin_convertvector(pv[2], bf16x2_t));
+      pk.w = __builtin_bit_cast(uint32_t, __builtin_convertvector(pv[3], bf16x2_t));
       pb[nt] = __builtin_bit_cast(bf16x8_t, pk);
     }
 
-    // make this wave's LDS writes visible to its own lanes before the reads
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    // the stage was written by this wave only: LDS executes a wave's
+    // operations in order, so a compiler barrier plus an LDS wait suffices
+    lds_wave_sync();
 
     // ---- O^T += V^T . P^T ; pair pp covers d = 32*pp + 2*m + {0 (even tile), 1 (odd tile)}
 #pragma unroll
@@ -332,10 +382,30 @@ paged_attention_kernel(AttnParams p) {
         acc[nt][2 * pp + 1] = mfma(oa, pb[nt], acc[nt][2 * pp + 1]);
       }
     }
-    // the next iteration overwrites the stage: finish these reads first
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+    // the next chunk overwrites the stage: its reads must be done first
+    lds_wave_sync();
+  };
+
+  // ---- software pipeline: the next chunk's loads are in flight while the
+  // current chunk is computed
+  Chunk cur, nxt;
+  int c = wave;
+  int cur_blk = -1;
+  if (c < nchunks) {
+    cur_blk = block_of(kv_begin + c * kChunk);
+    if (cur_blk >= 0) load(kv_begin + c * kChunk, cur_blk, cur);
+  }
+  for (; c < nchunks; c += kWaves) {
+    const int kb = kv_begin + c * kChunk;
+    const int cn = c + kWaves;
+    int nxt_blk = -1;
+    if (cn < nchunks) {
+      nxt_blk = block_of(kv_begin + cn * kChunk);
+      if (nxt_blk >= 0) load(kv_begin + cn * kChunk, nxt_blk, nxt);
+    }
+    if (cur_blk >= 0) process(kb, cur);
+    cur = nxt;
+    cur_blk = nxt_blk;
   }
 
   // ---- merge the four waves
