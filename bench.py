@@ -8,11 +8,14 @@ is accepted tok/s = tokens committed in the K timed steps / their wall time
 already prefilled (prefill is not timed).
 
 The same JSON line carries
-  roofline:      the verify attention kernel (K1), timed live with HIP events on
-                 its stream around every verify-attention launch of the timed
-                 steps; achieved = algorithmic bytes per launch / mean launch
-                 time, algorithmic bytes = sum_i L_i*Hkv*D*2B*2 (K and V read
-                 once) + T*Hq*D*2B*2 (Q in, O out);
+  roofline:      the verify attention kernel (K1), timed with HIP events on
+                 its stream around every verify-attention launch of
+                 --roofline-steps further steps of the same workload (the
+                 timed steps replay HIP graphs, inside which ROCm torch cannot
+                 record timing events, so these steps launch the verify
+                 forward eagerly); achieved = algorithmic bytes per launch /
+                 mean launch time, algorithmic bytes = sum_i L_i*Hkv*D*2B*2
+                 (K and V read once) + T*Hq*D*2B*2 (Q in, O out);
   cpu_baseline:  the reference's host acceptance logic (per-sequence bf16
                  argmax + .tolist() + verify_greedy_proposals) timed on this
                  host's cores over verify batches copied from the run.
@@ -51,6 +54,9 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="bound on the CPU-baseline sample's run time")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--roofline-steps", type=int, default=5,
+                    help="extra steps with the verify forward run eagerly so that every "
+                         "verify-attention launch is bracketed by HIP events")
     return ap.parse_args()
 
 
@@ -223,7 +229,6 @@ def main():
     n_active = len(llm.scheduler.running)
     before = dict(llm.spec_stats)
     committed = 0
-    timer.enabled = True
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
@@ -231,10 +236,20 @@ def main():
         committed += -num_tokens
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    timer.enabled = False
     elapsed = t1 - t0
-    roof = timer.result()
     stats = {k: llm.spec_stats[k] - before[k] for k in before}
+
+    # roofline: the same workload for a few more steps with the verify forward
+    # launched eagerly (events cannot be recorded inside a captured HIP graph
+    # on ROCm); the kernels and their inputs are those of the timed steps
+    runner.use_verify_graph = False
+    timer.enabled = True
+    for _ in range(args.roofline_steps):
+        llm.step()
+    torch.cuda.synchronize()
+    timer.enabled = False
+    runner.use_verify_graph = True
+    roof = timer.result()
 
     log(f"timed {args.steps} steps in {elapsed:.3f}s")
     cpu = None

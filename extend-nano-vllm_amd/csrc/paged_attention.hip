@@ -26,22 +26,24 @@
 // that covers the whole sequence writes bf16 output directly, otherwise it
 // writes a normalised fp32 partial plus its log-sum-exp, and a second kernel
 // merges the splits.
+#include <stdlib.h>
+
 #include "common.h"
 
 namespace nva {
 namespace {
 
 constexpr int kD = 128;
-constexpr int kWaves = 4;
-constexpr int kThreads = kWaves * kWave;
+constexpr int kCombineWaves = 4;
+constexpr int kCombineThreads = kCombineWaves * kWave;
 constexpr int kChunk = 32;
 constexpr int kVPitch = 68;                          // dwords per staged V row
-constexpr int kVStage = kChunk * kVPitch;            // dwords per wave
-constexpr int kAccPitch = kD + 4;                    // floats per column in the merge tile
-constexpr int kLdsDwords = kWaves * kVStage + 2 * kWaves * 64;
-static_assert(kWaves * 16 * kAccPitch <= kWaves * kVStage, "merge tile must fit the V stages");
-constexpr int kTargetWorkgroups = 2048;
+constexpr int kVStage = kChunk * kVPitch;            // dwords of the wave's V stage
+constexpr int kAccPitch = kD + 4;                    // floats per column in the output tile
+static_assert(16 * kAccPitch + 16 <= kVStage, "output tile must fit the V stage");
+constexpr int kSplitKeys = 768;
 constexpr int kMinSplit = 128;
+constexpr int64_t kMinWorkgroups = 1024;
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleSlack = 8.0f;   // log2 headroom before the running max moves
 
@@ -120,17 +122,18 @@ __device__ __forceinline__ void seq_geometry(const AttnParams& p, int seq, int& 
   L = L > p.max_k ? p.max_k : L;
 }
 
+// two waves per SIMD fit the register budget of tiles up to 32 columns;
+// 64-column tiles (NT = 4) need the full register file of one wave
 template <int NT, bool FP8>
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kWave, NT >= 4 ? 1 : 2)
 paged_attention_kernel(AttnParams p) {
-  __shared__ __attribute__((aligned(16))) uint32_t lds[kLdsDwords];
+  __shared__ __attribute__((aligned(16))) uint32_t vst[kVStage];
 
   const int split = blockIdx.x % p.max_splits;
   const int qt = blockIdx.x / p.max_splits;
   const int kvh = blockIdx.y;
   const int seq = blockIdx.z;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const int lane = threadIdx.x & (kWave - 1);
+  const int lane = threadIdx.x;
   const int g = lane >> 4;
   const int m16 = lane & 15;
 
@@ -147,7 +150,7 @@ paged_attention_kernel(AttnParams p) {
   if (kv_limit <= 0) {
     // nothing visible: zero output rows (once, from split 0)
     if (split != 0) return;
-    for (int idx = threadIdx.x; idx < rows * (kD / 8); idx += kThreads) {
+    for (int idx = lane; idx < rows * (kD / 8); idx += kWave) {
       const int n = idx / (kD / 8), dv = idx % (kD / 8);
       const int j = j0 + n / p.group, hh = n % p.group;
       uint16_t* o = p.out + static_cast<int64_t>(q_start + j) * p.out_row_stride +
@@ -198,7 +201,6 @@ paged_attention_kernel(AttnParams p) {
     for (int t = 0; t < 8; ++t) acc[nt][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
   }
 
-  uint32_t* vst = lds + wave * kVStage;
   const int nchunks = (kv_end - kv_begin + kChunk - 1) / kChunk;
   const int32_t* bt = p.block_tables + static_cast<int64_t>(seq) * p.bt_stride;
   constexpr int64_t esz = FP8 ? 1 : 2;
@@ -209,27 +211,19 @@ paged_attention_kernel(AttnParams p) {
   const int nblk = (kv_end - 1) / p.block_size - first_blk + 1;
   int lane_blk = -1;
   if (lane < nblk && first_blk + lane < p.bt_cols) lane_blk = bt[first_blk + lane];
-  auto block_of = [&](int kb) -> int {
-    const int lb = kb / p.block_size;
-    const int rel = lb - first_blk;
-    int b;
-    if (rel < kWave)
-      b = __builtin_amdgcn_readlane(lane_blk, rel);
-    else
-      b = lb < p.bt_cols ? bt[lb] : -1;
-    return (b >= 0 && b < p.num_blocks) ? b : -1;   // invalid block: keys masked
-  };
 
-  // Raw K / V registers of one 32-key chunk.  K: lane holds key (16*kt + m16),
-  // head_dim elements 32*s + 8*g .. +7; V: coalesced rows for the LDS stage.
-  struct Chunk {
-    uint4 k[2][4];     // fp8 uses .x/.y only
-    uint4 v[8];        // fp8 uses v[0..3]
-  };
-  auto load = [&](int kb, int pblk, Chunk& r) {
+  for (int c = 0; c < nchunks; ++c) {
+    const int kb = kv_begin + c * kChunk;
+    const int lb = kb / p.block_size;
+    int pblk = (lb - first_blk < kWave) ? __builtin_amdgcn_readlane(lane_blk, lb - first_blk)
+                                        : (lb < p.bt_cols ? bt[lb] : -1);
+    if (pblk < 0 || pblk >= p.num_blocks) continue;   // invalid block: keys masked
     const int off0 = kb % p.block_size;
     const int64_t blk_base = static_cast<int64_t>(pblk) * p.blk_stride +
                              static_cast<int64_t>(kvh) * p.head_stride;
+
+    // ---- K operands straight from the cache: key (16*kt + m16), d 32*s + 8*g .. +7
+    uint4 kraw[2][4];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
       int key = kb + kt * 16 + m16;
@@ -239,19 +233,24 @@ paged_attention_kernel(AttnParams p) {
       for (int s = 0; s < 4; ++s) {
         if (FP8) {
           const uint2 w = *reinterpret_cast<const uint2*>(p.k_cache + (e + 32 * s + 8 * g));
-          r.k[kt][s] = make_uint4(w.x, w.y, 0, 0);
+          kraw[kt][s] = make_uint4(w.x, w.y, 0, 0);
         } else {
-          r.k[kt][s] = *reinterpret_cast<const uint4*>(p.k_cache + (e + 32 * s + 8 * g) * esz);
+          kraw[kt][s] = *reinterpret_cast<const uint4*>(p.k_cache + (e + 32 * s + 8 * g) * esz);
         }
       }
     }
+    // ---- V rows (coalesced) into the wave's LDS stage
     if (FP8) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        int key = kb + 8 * i + (lane >> 3);
+        const int row = 8 * i + (lane >> 3);
+        int key = kb + row;
         key = key < kv_limit ? key : kv_limit - 1;
         const int64_t e = blk_base + static_cast<int64_t>(off0 + key - kb) * p.tok_stride + (lane & 7) * 16;
-        r.v[i] = *reinterpret_cast<const uint4*>(p.v_cache + e);
+        const uint4 w = *reinterpret_cast<const uint4*>(p.v_cache + e);
+        uint32_t* dst = vst + row * kVPitch + (lane & 7) * 8;
+        *reinterpret_cast<bf16x8_t*>(dst) = fp8x8_to_bf16(make_uint2(w.x, w.y));
+        *reinterpret_cast<bf16x8_t*>(dst + 4) = fp8x8_to_bf16(make_uint2(w.z, w.w));
       }
     } else {
 #pragma unroll
@@ -259,25 +258,9 @@ paged_attention_kernel(AttnParams p) {
         int key = kb + 4 * i + g;
         key = key < kv_limit ? key : kv_limit - 1;
         const int64_t e = blk_base + static_cast<int64_t>(off0 + key - kb) * p.tok_stride + m16 * 8;
-        r.v[i] = *reinterpret_cast<const uint4*>(p.v_cache + e * esz);
+        *reinterpret_cast<uint4*>(vst + (4 * i + g) * kVPitch + m16 * 4) =
+            *reinterpret_cast<const uint4*>(p.v_cache + e * esz);
       }
-    }
-  };
-
-  auto process = [&](int kb, const Chunk& r) {
-    // ---- V rows into the wave's LDS stage
-    if (FP8) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = 8 * i + (lane >> 3);
-        uint32_t* dst = vst + row * kVPitch + (lane & 7) * 8;
-        *reinterpret_cast<bf16x8_t*>(dst) = fp8x8_to_bf16(make_uint2(r.v[i].x, r.v[i].y));
-        *reinterpret_cast<bf16x8_t*>(dst + 4) = fp8x8_to_bf16(make_uint2(r.v[i].z, r.v[i].w));
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 8; ++i)
-        *reinterpret_cast<uint4*>(vst + (4 * i + g) * kVPitch + m16 * 4) = r.v[i];
     }
 
     // ---- S^T = K . Q^T
@@ -287,8 +270,8 @@ paged_attention_kernel(AttnParams p) {
       bf16x8_t kop[4];
 #pragma unroll
       for (int s = 0; s < 4; ++s)
-        kop[s] = FP8 ? fp8x8_to_bf16(make_uint2(r.k[kt][s].x, r.k[kt][s].y))
-                     : __builtin_bit_cast(bf16x8_t, r.k[kt][s]);
+        kop[s] = FP8 ? fp8x8_to_bf16(make_uint2(kraw[kt][s].x, kraw[kt][s].y))
+                     : __builtin_bit_cast(bf16x8_t, kraw[kt][s]);
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         f32x4_t a = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -384,123 +367,75 @@ paged_attention_kernel(AttnParams p) {
     }
     // the next chunk overwrites the stage: its reads must be done first
     lds_wave_sync();
-  };
-
-  // ---- software pipeline: the next chunk's loads are in flight while the
-  // current chunk is computed
-  Chunk cur, nxt;
-  int c = wave;
-  int cur_blk = -1;
-  if (c < nchunks) {
-    cur_blk = block_of(kv_begin + c * kChunk);
-    if (cur_blk >= 0) load(kv_begin + c * kChunk, cur_blk, cur);
-  }
-  for (; c < nchunks; c += kWaves) {
-    const int kb = kv_begin + c * kChunk;
-    const int cn = c + kWaves;
-    int nxt_blk = -1;
-    if (cn < nchunks) {
-      nxt_blk = block_of(kv_begin + cn * kChunk);
-      if (nxt_blk >= 0) load(kv_begin + cn * kChunk, nxt_blk, nxt);
-    }
-    if (cur_blk >= 0) process(kb, cur);
-    cur = nxt;
-    cur_blk = nxt_blk;
   }
 
-  // ---- merge the four waves
+  // ---- finish: per column sum, transpose O^T through LDS, 16-byte stores.
+  float* tile = reinterpret_cast<float*>(vst);               // [16 cols][kAccPitch]
+  float* col_l = tile + 16 * kAccPitch;                      // [16]
+  const int ccol = lane >> 2;                                // column handled on output
+  const int dq = lane & 3;                                   // 32 consecutive d
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    l_run[nt] += __shfl_xor(l_run[nt], 16, kWave);
-    l_run[nt] += __shfl_xor(l_run[nt], 32, kWave);
-  }
-  float* sm_m = reinterpret_cast<float*>(lds + kWaves * kVStage);
-  float* sm_l = sm_m + kWaves * 64;
-  float* sacc_lds = reinterpret_cast<float*>(lds);   // [wave][16 cols][kAccPitch]
-  __syncthreads();
-  if (g == 0) {
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      sm_m[wave * 64 + nt * 16 + m16] = m_run[nt];
-      sm_l[wave * 64 + nt * 16 + m16] = l_run[nt];
-    }
-  }
-  __syncthreads();
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    const int col = nt * 16 + m16;
-    float M = -INFINITY;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w * 64 + col]);
-    const float f = (m_run[nt] == -INFINITY) ? 0.0f : exp2f_fast(m_run[nt] - M);
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[nt][t][i] *= f;
-    }
-  }
-
-  const int ccol = threadIdx.x >> 4;          // 0..15: column within the N tile
-  const int dgrp = threadIdx.x & 15;          // 8 consecutive d per thread
-#pragma unroll
-  for (int nt = 0; nt < NT; ++nt) {
-    // scatter this wave's O^T tile as [col][d] floats
+    float l = l_run[nt];
+    l += __shfl_xor(l, 16, kWave);
+    l += __shfl_xor(l, 32, kWave);
 #pragma unroll
     for (int pp = 0; pp < 4; ++pp) {
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int d = 32 * pp + 2 * (4 * g + i) + e;
-          sacc_lds[(wave * 16 + m16) * kAccPitch + d] = acc[nt][2 * pp + e][i];
-        }
+        for (int i = 0; i < 4; ++i) tile[m16 * kAccPitch + 32 * pp + 2 * (4 * g + i) + e] = acc[nt][2 * pp + e][i];
       }
     }
-    __syncthreads();
+    if (g == 0) col_l[m16] = l;
+    lds_wave_sync();
     const int n = nt * 16 + ccol;
     if (n < rows) {
-      float M = -INFINITY;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w * 64 + n]);
-      float ltot = 0.0f;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        const float mw = sm_m[w * 64 + n];
-        ltot += (mw == -INFINITY) ? 0.0f : sm_l[w * 64 + n] * exp2f_fast(mw - M);
-      }
-      float o[8];
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        float s = 0.0f;
-#pragma unroll
-        for (int w = 0; w < kWaves; ++w) s += sacc_lds[(w * 16 + ccol) * kAccPitch + dgrp * 8 + k];
-        o[k] = ltot > 0.0f ? s / ltot * vscale : 0.0f;
-      }
+      const float lt = col_l[ccol];
+      const float inv = lt > 0.0f ? vscale / lt : 0.0f;
+      const float* src = tile + ccol * kAccPitch + dq * 32;
       const int j = j0 + n / p.group, hh = n % p.group;
       const int t = q_start + j;
       const int h = kvh * p.group + hh;
       if (nsplit == 1) {
         uint16_t* op = p.out + static_cast<int64_t>(t) * p.out_row_stride +
-                       static_cast<int64_t>(h) * p.out_head_stride + dgrp * 8;
-        *reinterpret_cast<uint4*>(op) = make_uint4(pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]),
-                                                   pack_bf16(o[4], o[5]), pack_bf16(o[6], o[7]));
+                       static_cast<int64_t>(h) * p.out_head_stride + dq * 32;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const float* a = src + 8 * v;
+          *reinterpret_cast<uint4*>(op + 8 * v) =
+              make_uint4(pack_bf16(a[0] * inv, a[1] * inv), pack_bf16(a[2] * inv, a[3] * inv),
+                         pack_bf16(a[4] * inv, a[5] * inv), pack_bf16(a[6] * inv, a[7] * inv));
+        }
       } else {
         const int64_t slot = (static_cast<int64_t>(t) * p.hq + h) * p.max_splits + split;
-        float* wo = p.ws_o + slot * kD + dgrp * 8;
-        *reinterpret_cast<float4*>(wo) = make_float4(o[0], o[1], o[2], o[3]);
-        *reinterpret_cast<float4*>(wo + 4) = make_float4(o[4], o[5], o[6], o[7]);
-        if (dgrp == 0) p.ws_lse[slot] = ltot > 0.0f ? M + __log2f(ltot) : -INFINITY;
+        float* wo = p.ws_o + slot * kD + dq * 32;
+#pragma unroll
+        for (int v = 0; v < 8; ++v)
+          *reinterpret_cast<float4*>(wo + 4 * v) =
+              make_float4(src[4 * v] * inv, src[4 * v + 1] * inv, src[4 * v + 2] * inv, src[4 * v + 3] * inv);
       }
     }
-    __syncthreads();
+    // log-sum-exp (log2 domain) of each column: lanes with g == 0 hold the
+    // column's running max and sum
+    if (nsplit > 1 && g == 0) {
+      const int n2 = nt * 16 + m16;
+      if (n2 < rows) {
+        const int j = j0 + n2 / p.group, hh = n2 % p.group;
+        const int64_t slot = (static_cast<int64_t>(q_start + j) * p.hq + kvh * p.group + hh) *
+                                 p.max_splits + split;
+        p.ws_lse[slot] = l > 0.0f ? m_run[nt] + __log2f(l) : -INFINITY;
+      }
+    }
+    lds_wave_sync();
   }
 }
 
 // Merge split partials: one wave per (token row, q head); lane covers 2 d.
-__global__ void __launch_bounds__(kThreads)
+__global__ void __launch_bounds__(kCombineThreads)
 combine_kernel(AttnParams p) {
   const int t = blockIdx.x;
-  const int h = blockIdx.y * kWaves + threadIdx.x / kWave;
+  const int h = blockIdx.y * kCombineWaves + threadIdx.x / kWave;
   const int lane = threadIdx.x & (kWave - 1);
   if (h >= p.hq || t >= p.num_tokens) return;
   int seq;
@@ -550,17 +485,23 @@ int32_t choose_qtile(int32_t max_q, int32_t group) {
   return max_q < qtile ? (max_q > 0 ? max_q : 1) : qtile;
 }
 
+// Split length: 768 keys (three 256-token blocks) balances work per wave
+// against the split-combine traffic on the measured configs; it shrinks (to a
+// 128-key minimum) only when fewer than kMinWorkgroups would be launched.
 void choose_split(int32_t num_seqs, int32_t num_kv_heads, int32_t n_qtiles, int32_t max_k,
                   int32_t* split_len, int32_t* max_splits) {
   const int64_t base = static_cast<int64_t>(num_seqs > 0 ? num_seqs : 1) *
                        (num_kv_heads > 0 ? num_kv_heads : 1) * (n_qtiles > 0 ? n_qtiles : 1);
-  int64_t want = (kTargetWorkgroups + base - 1) / base;
   const int32_t mk = max_k > 1 ? max_k : 1;
-  int64_t by_len = (mk + kMinSplit - 1) / kMinSplit;
-  int64_t s = want < by_len ? want : by_len;
-  if (s < 1) s = 1;
-  int32_t len = static_cast<int32_t>((mk + s - 1) / s);
-  len = (len + kMinSplit - 1) / kMinSplit * kMinSplit;
+  int32_t len = kSplitKeys;
+  while (len > kMinSplit && base * ((mk + len - 1) / len) < kMinWorkgroups) len -= kMinSplit;
+  // NVA_ATTN_SPLIT_KEYS (a multiple of 128) fixes the split length for tuning
+  static const int32_t forced = [] {
+    const char* v = getenv("NVA_ATTN_SPLIT_KEYS");
+    const int32_t f = v ? atoi(v) : 0;
+    return (f > 0 && f % kMinSplit == 0) ? f : 0;
+  }();
+  if (forced) len = forced;
   *split_len = len;
   *max_splits = (mk + len - 1) / len;
 }
@@ -579,9 +520,9 @@ size_t workspace_bytes(int32_t num_seqs, int32_t num_tokens, int32_t hq, int32_t
 template <int NT>
 void launch_nt(const AttnParams& p, bool fp8, dim3 grid, hipStream_t s) {
   if (fp8)
-    paged_attention_kernel<NT, true><<<grid, kThreads, 0, s>>>(p);
+    paged_attention_kernel<NT, true><<<grid, kWave, 0, s>>>(p);
   else
-    paged_attention_kernel<NT, false><<<grid, kThreads, 0, s>>>(p);
+    paged_attention_kernel<NT, false><<<grid, kWave, 0, s>>>(p);
 }
 
 int run_attention(AttnParams& p, int kv_dtype, void* workspace, size_t workspace_bytes_, hipStream_t s) {
@@ -625,8 +566,8 @@ int run_attention(AttnParams& p, int kv_dtype, void* workspace, size_t workspace
     launch_nt<4>(p, fp8, grid, s);
   if (hipGetLastError() != hipSuccess) return NVA_ERR_LAUNCH;
   if (p.max_splits > 1) {
-    dim3 cgrid(p.num_tokens, (p.hq + kWaves - 1) / kWaves);
-    combine_kernel<<<cgrid, kThreads, 0, s>>>(p);
+    dim3 cgrid(p.num_tokens, (p.hq + kCombineWaves - 1) / kCombineWaves);
+    combine_kernel<<<cgrid, kCombineThreads, 0, s>>>(p);
   }
   return launch_status();
 }

@@ -1,0 +1,269 @@
+"""HIP-graph captures of the three device stages of a speculative step.
+
+Each graph is captured once per padded batch size (bucket) on first use and
+replayed with its static metadata buffers refreshed by one host->device copy
+per dtype.  Padded sequences have slot -1 (no K/V write) and block id -1 (no
+K/V read), so they cost compute but touch no cache state.  Steps the graphs
+do not cover (ragged proposal counts near max_tokens, ragged commits) run
+eagerly; results are identical either way.
+
+  VerifyGraph   target forward over q = k+1 rows per sequence, all-row LM
+                head, fused argmax + accept      (model_runner.py:1047-1078)
+  ProposeGraph  k greedy draft tokens: sample, then k-1 draft decode steps
+                                                  (model_runner.py:1159-1213)
+  CommitGraph   draft replay of n committed tokens per sequence, aux rows
+                gathered from the VerifyGraph's static aux states
+                                                  (model_runner.py:1216-1249)
+"""
+from __future__ import annotations
+
+import torch
+
+from nanovllm_amd import kernels as K
+from nanovllm_amd.context import reset_context, set_context
+from nanovllm_amd.qwen3 import aux_concat
+
+BUCKETS = (1, 2, 4, 8, 16, 24, 32, 48, 64, 96, 128, 192, 256, 384, 512)
+
+
+def bucket_for(n: int) -> int | None:
+    for b in BUCKETS:
+        if b >= n:
+            return b
+    return None
+
+
+class _Staging:
+    """A device buffer plus a pinned host twin of the same dtype; fields are
+    contiguous slices of both."""
+
+    def __init__(self, sizes: dict[str, int], dtype: torch.dtype, device: torch.device):
+        total = sum(sizes.values())
+        self.host = torch.zeros(max(total, 1), dtype=dtype, pin_memory=True)
+        self.dev = torch.zeros(max(total, 1), dtype=dtype, device=device)
+        self.fields: dict[str, tuple[int, int]] = {}
+        off = 0
+        for name, n in sizes.items():
+            self.fields[name] = (off, n)
+            off += n
+        self.total = total
+
+    def dev_view(self, name: str) -> torch.Tensor:
+        off, n = self.fields[name]
+        return self.dev[off:off + n]
+
+    def fill(self, name: str, values) -> None:
+        off, n = self.fields[name]
+        t = torch.as_tensor(values, dtype=self.host.dtype)
+        if t.numel() != n:
+            raise ValueError(f"{name}: {t.numel()} values for {n} slots")
+        self.host[off:off + n].copy_(t.reshape(-1))
+
+    def upload(self) -> None:
+        self.dev[:self.total].copy_(self.host[:self.total], non_blocking=True)
+
+
+class _GraphBase:
+
+    def __init__(self, runner):
+        self.runner = runner
+        self.device = runner.device
+        self.graph = torch.cuda.CUDAGraph()
+
+    def _capture(self, body) -> None:
+        """Eager run (allocates workspaces, compiles nothing), then capture."""
+        body()
+        torch.cuda.synchronize(self.device)
+        with torch.cuda.graph(self.graph, pool=self.runner.graph_pool):
+            body()
+        if self.runner.graph_pool is None:
+            self.runner.graph_pool = self.graph.pool()
+        torch.cuda.synchronize(self.device)
+
+
+class VerifyGraph(_GraphBase):
+
+    def __init__(self, runner, bs: int, q: int):
+        super().__init__(runner)
+        self.bs, self.q, self.T = bs, q, bs * q
+        T = self.T
+        self.max_blocks = runner.max_blocks_per_seq
+        self.i64 = _Staging({"ids": T, "pos": T}, torch.int64, self.device)
+        self.i32 = _Staging({"cu_q": bs + 1, "cu_k": bs + 1, "slots": T,
+                             "bt": bs * self.max_blocks}, torch.int32, self.device)
+        self.out = torch.zeros(T + 2 * bs, dtype=torch.int32, device=self.device)
+        self.aux = None
+        # valid dummy metadata for the capture run
+        self._fill_dummy()
+        self._capture(self._body)
+
+    def _fill_dummy(self):
+        bs, q = self.bs, self.q
+        self.i64.fill("ids", [0] * self.T)
+        self.i64.fill("pos", [j for _ in range(bs) for j in range(q)])
+        self.i32.fill("cu_q", [i * q for i in range(bs + 1)])
+        self.i32.fill("cu_k", [i * q for i in range(bs + 1)])
+        self.i32.fill("slots", [-1] * self.T)
+        self.i32.fill("bt", [-1] * (bs * self.max_blocks))
+        self.i64.upload()
+        self.i32.upload()
+
+    def _body(self):
+        r = self.runner
+        ids = self.i64.dev_view("ids")
+        set_context(True, self.i32.dev_view("cu_q"), self.i32.dev_view("cu_k"), self.q,
+                    r.max_seqlen_k, self.i32.dev_view("slots"), None,
+                    self.i32.dev_view("bt").view(self.bs, self.max_blocks))
+        try:
+            hidden, aux = r.model.forward_with_aux_hidden_states(
+                ids, self.i64.dev_view("pos"), r.speculative_config.aux_hidden_state_layers)
+            logits = r.model.compute_all_logits(hidden)
+            K.argmax_accept(logits, self.i32.dev_view("cu_q"), ids, out=self.out)
+            self.aux = aux
+        finally:
+            reset_context()
+
+    def run(self, ids, pos, cu_q, cu_k, slots, bt_rows) -> None:
+        """Host lists for the real sequences; the rest of the bucket is padding."""
+        bs, q, T = self.bs, self.q, self.T
+        n = len(ids)
+        b = len(cu_q) - 1
+        self.i64.fill("ids", list(ids) + [0] * (T - n))
+        self.i64.fill("pos", list(pos) + [0] * (T - n))
+        pad_cu = [cu_q[-1] + q * (i + 1) for i in range(bs - b)]
+        self.i32.fill("cu_q", list(cu_q) + pad_cu)
+        self.i32.fill("cu_k", list(cu_k) + [cu_k[-1] + q * (i + 1) for i in range(bs - b)])
+        self.i32.fill("slots", list(slots) + [-1] * (T - n))
+        flat = []
+        for row in bt_rows:
+            flat.extend(row + [-1] * (self.max_blocks - len(row)))
+        flat.extend([-1] * (self.max_blocks * (bs - b)))
+        self.i32.fill("bt", flat)
+        self.i64.upload()
+        self.i32.upload()
+        self.graph.replay()
+
+
+class ProposeGraph(_GraphBase):
+
+    def __init__(self, runner, bs: int, k: int):
+        super().__init__(runner)
+        self.bs, self.k = bs, k
+        r = runner
+        h = r.eagle3_model.config.hidden_size
+        self.max_blocks = r.max_blocks_per_seq
+        steps = max(k - 1, 1)
+        self.hidden = torch.zeros(bs, h, dtype=r.dtype, device=self.device)
+        self.feedback = torch.zeros(bs, h, dtype=r.dtype, device=self.device)
+        self.tokens = torch.zeros(k, bs, dtype=torch.int64, device=self.device)
+        self.i64 = _Staging({"pos": steps * bs}, torch.int64, self.device)
+        self.i32 = _Staging({"slots": steps * bs, "ctx": steps * bs, "bt": bs * self.max_blocks},
+                            torch.int32, self.device)
+        self.i64.fill("pos", [0] * (steps * bs))
+        self.i32.fill("slots", [-1] * (steps * bs))
+        self.i32.fill("ctx", [1] * (steps * bs))
+        self.i32.fill("bt", [-1] * (bs * self.max_blocks))
+        self.i64.upload()
+        self.i32.upload()
+        self._capture(self._body)
+
+    def _body(self):
+        r = self.runner
+        draft = r.eagle3_model
+        bs = self.bs
+        pos = self.i64.dev_view("pos").view(-1, bs)
+        slots = self.i32.dev_view("slots").view(-1, bs)
+        ctx = self.i32.dev_view("ctx").view(-1, bs)
+        bt = self.i32.dev_view("bt").view(bs, self.max_blocks)
+        draft.sample_greedy(self.hidden, out=self.tokens[0])
+        feedback = self.feedback
+        try:
+            for s in range(self.k - 1):
+                set_context(False, slot_mapping=slots[s], context_lens=ctx[s], block_tables=bt,
+                            max_seqlen_k=r.max_seqlen_k)
+                hidden, feedback = draft.forward_with_cache(self.tokens[s], pos[s], feedback)
+                draft.sample_greedy(hidden, out=self.tokens[s + 1])
+        finally:
+            reset_context()
+
+    def run(self, state_slots: torch.Tensor, pos, slots, ctx, bt_rows) -> torch.Tensor:
+        """state_slots: device int64 [b] rows of the runner's draft-state table.
+        pos/slots/ctx: host lists [k-1][b].  Returns tokens [k, bs] (device)."""
+        r = self.runner
+        b = state_slots.numel()
+        bs = self.bs
+        torch.index_select(r.state_hidden, 0, state_slots, out=self.hidden[:b])
+        torch.index_select(r.state_feedback, 0, state_slots, out=self.feedback[:b])
+        pad = bs - b
+        self.i64.fill("pos", [v for row in pos for v in (list(row) + [0] * pad)])
+        self.i32.fill("slots", [v for row in slots for v in (list(row) + [-1] * pad)])
+        self.i32.fill("ctx", [v for row in ctx for v in (list(row) + [1] * pad)])
+        flat = []
+        for row in bt_rows:
+            flat.extend(row + [-1] * (self.max_blocks - len(row)))
+        flat.extend([-1] * (self.max_blocks * pad))
+        self.i32.fill("bt", flat)
+        self.i64.upload()
+        self.i32.upload()
+        self.graph.replay()
+        return self.tokens
+
+
+class CommitGraph(_GraphBase):
+    """n committed tokens for each of bs sequences whose aux rows live in
+    ``verify.aux`` (the verify graph of the same bucket)."""
+
+    def __init__(self, runner, verify: VerifyGraph, n: int):
+        super().__init__(runner)
+        self.verify = verify
+        self.bs, self.n = verify.bs, n
+        R = self.bs * n
+        self.R = R
+        self.max_blocks = runner.max_blocks_per_seq
+        self.i64 = _Staging({"ids": R, "pos": R}, torch.int64, self.device)
+        self.i32 = _Staging({"rows": R, "cu_q": self.bs + 1, "cu_k": self.bs + 1, "slots": R,
+                             "bt": self.bs * self.max_blocks}, torch.int32, self.device)
+        self.i64.fill("ids", [0] * R)
+        self.i64.fill("pos", [j for _ in range(self.bs) for j in range(n)])
+        self.i32.fill("rows", [-1] * R)
+        self.i32.fill("cu_q", [i * n for i in range(self.bs + 1)])
+        self.i32.fill("cu_k", [i * n for i in range(self.bs + 1)])
+        self.i32.fill("slots", [-1] * R)
+        self.i32.fill("bt", [-1] * (self.bs * self.max_blocks))
+        self.i64.upload()
+        self.i32.upload()
+        self.hidden = self.feedback = None
+        self._capture(self._body)
+
+    def _body(self):
+        r = self.runner
+        draft = r.eagle3_model
+        combined = draft.combine_hidden_states(aux_concat(self.verify.aux,
+                                                          self.i32.dev_view("rows")))
+        set_context(True, self.i32.dev_view("cu_q"), self.i32.dev_view("cu_k"), self.n,
+                    r.max_seqlen_k, self.i32.dev_view("slots"), None,
+                    self.i32.dev_view("bt").view(self.bs, self.max_blocks))
+        try:
+            self.hidden, self.feedback = draft.forward_with_cache(
+                self.i64.dev_view("ids"), self.i64.dev_view("pos"), combined)
+        finally:
+            reset_context()
+
+    def run(self, rows, ids, pos, cu_q, cu_k, slots, bt_rows) -> None:
+        R, bs, n = self.R, self.bs, self.n
+        m = len(ids)
+        b = len(cu_q) - 1
+        self.i32.fill("rows", list(rows) + [-1] * (R - m))
+        self.i64.fill("ids", list(ids) + [0] * (R - m))
+        self.i64.fill("pos", list(pos) + [0] * (R - m))
+        self.i32.fill("cu_q", list(cu_q) + [cu_q[-1] + n * (i + 1) for i in range(bs - b)])
+        self.i32.fill("cu_k", list(cu_k) + [cu_k[-1] + n * (i + 1) for i in range(bs - b)])
+        self.i32.fill("slots", list(slots) + [-1] * (R - m))
+        flat = []
+        for row in bt_rows:
+            flat.extend(row + [-1] * (self.max_blocks - len(row)))
+        flat.extend([-1] * (self.max_blocks * (bs - b)))
+        self.i32.fill("bt", flat)
+        self.i64.upload()
+        self.i32.upload()
+        self.graph.replay()

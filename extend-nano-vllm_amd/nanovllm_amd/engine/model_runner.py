@@ -26,6 +26,7 @@ from nanovllm_amd import _native
 from nanovllm_amd import kernels as K
 from nanovllm_amd.context import get_context, reset_context, set_context
 from nanovllm_amd.eagle3 import Eagle3KVCache, load_eagle3_model
+from nanovllm_amd.engine.graphs import CommitGraph, ProposeGraph, VerifyGraph, bucket_for
 from nanovllm_amd.engine.sequence import Sequence
 from nanovllm_amd.layers import Attention, init_random_, param_bytes
 from nanovllm_amd.loader import load_model
@@ -67,11 +68,15 @@ class ModelRunner:
             self.model.eval()
             self.speculative_config = config.speculative_config
             self.eagle3_model = None
-            self.eagle3_states: dict[int, Eagle3KVCache] = {}
             self.eagle_graphs: dict = {}
             self.eagle_graph_vars: dict = {}
             self.graphs: dict = {}
+            self.graph_pool = None
+            self._verify_graphs: dict[int, VerifyGraph] = {}
+            self._propose_graphs: dict[int, ProposeGraph] = {}
+            self._commit_graphs: dict[tuple[int, int], CommitGraph] = {}
             self._pending_verify = None
+            self._pending_graph = None
             if self.speculative_config is not None:
                 self.eagle3_model = load_eagle3_model(self.speculative_config.model, self.device,
                                                       config.load_format, config.seed + 1)
@@ -82,11 +87,25 @@ class ModelRunner:
                     raise ValueError("EAGLE3 aux state count does not match aux_hidden_state_layers")
             self.warmup_model()
             self.allocate_kv_cache()
+            k = self.speculative_config.num_speculative_tokens if self.speculative_config else 0
+            # upper bounds of one sequence's keys and block-table width
+            self.max_seqlen_k = config.max_model_len + k + 1
+            self.max_blocks_per_seq = -(-self.max_seqlen_k // self.block_size)
+            if self.eagle3_model is not None:
+                # recurrent draft state of every running sequence, one row each
+                h = self.eagle3_model.config.hidden_size
+                rows = config.max_num_seqs + 1
+                self.state_hidden = torch.zeros(rows, h, dtype=self.dtype, device=self.device)
+                self.state_feedback = torch.zeros(rows, h, dtype=self.dtype, device=self.device)
+                self._state_slot: dict[int, int] = {}
+                self._free_state = list(range(rows - 1, -1, -1))
         finally:
             torch.set_default_device("cpu")
             torch.set_default_dtype(default_dtype)
-        # benchmarks may ask to keep the last verify's logits and inputs
+        # benchmarks may ask to keep the last verify's logits and inputs, or to
+        # run the verify forward eagerly (kernel-level timing)
         self.keep_verify_inputs = False
+        self.use_verify_graph = True
         self.last_verify_inputs = None
         # one pinned host buffer receives argmax + accept results each verify
         self._verify_host = torch.empty(1 << 16, dtype=torch.int32, pin_memory=True)
@@ -100,14 +119,42 @@ class ModelRunner:
             raise AttributeError(f"ModelRunner has no method {method_name!r}")
         return method(*args)
 
+    @property
+    def eagle3_states(self) -> dict[int, Eagle3KVCache]:
+        """Per-sequence draft state (views into the state table)."""
+        return {sid: Eagle3KVCache(self.state_hidden[r:r + 1], self.state_feedback[r:r + 1])
+                for sid, r in self._state_slot.items()}
+
+    def _state_rows(self, seqs) -> list[int]:
+        rows = []
+        for seq in seqs:
+            r = self._state_slot.get(seq.seq_id)
+            if r is None:
+                if not self._free_state:
+                    raise RuntimeError("no free EAGLE3 draft-state rows")
+                r = self._free_state.pop()
+                self._state_slot[seq.seq_id] = r
+            rows.append(r)
+        return rows
+
+    def _store_states(self, seqs, hidden, feedback, last_rows: list[int]) -> None:
+        dst = _pinned(self._state_rows(seqs), torch.int64).to(self.device, non_blocking=True)
+        src = _pinned(last_rows, torch.int64).to(self.device, non_blocking=True)
+        self.state_hidden.index_copy_(0, dst, hidden.index_select(0, src))
+        self.state_feedback.index_copy_(0, dst, feedback.index_select(0, src))
+
     def exit(self):
         if self._exited:
             return
         self._exited = True
+        torch.cuda.synchronize(self.device)
         self.graphs.clear()
         self.eagle_graphs.clear()
         self.eagle_graph_vars.clear()
-        torch.cuda.synchronize(self.device)
+        self._pending_graph = None
+        self._commit_graphs.clear()
+        self._verify_graphs.clear()
+        self._propose_graphs.clear()
 
     # ------------------------------------------------------------ memory
 
@@ -306,10 +353,7 @@ class ModelRunner:
         eagle_ids = _pinned(shifted, torch.int64).to(self.device, non_blocking=True)
         combined = self.eagle3_model.combine_hidden_states(aux_concat(aux))
         d_hidden, d_feedback = self.eagle3_model.forward_with_cache(eagle_ids, positions, combined)
-        for i, seq in enumerate(seqs):
-            r = cu[i + 1] - 1
-            self.eagle3_states[seq.seq_id] = Eagle3KVCache(d_hidden[r:r + 1].clone(),
-                                                           d_feedback[r:r + 1].clone())
+        self._store_states(seqs, d_hidden, d_feedback, [cu[i + 1] - 1 for i in range(len(seqs))])
         return next_host
 
     # ------------------------------------------------------------ EAGLE3
@@ -318,31 +362,51 @@ class ModelRunner:
         return {
             "paged_kv_cache": bool(getattr(self, "eagle3_model", None) is not None
                                    and getattr(self, "eagle_kv_cache", None) is not None),
-            "cuda_graph": bool(getattr(self, "eagle_graphs", {})),
-            "graph_batch_sizes": sorted(getattr(self, "eagle_graphs", {})),
+            "cuda_graph": bool(getattr(self, "eagle_graphs", {})
+                               or getattr(self, "_propose_graphs", {})),
+            "graph_batch_sizes": sorted(set(getattr(self, "eagle_graphs", {}))
+                                        | set(getattr(self, "_propose_graphs", {}))),
         }
+
+    def _use_graphs(self) -> bool:
+        return not self.enforce_eager
 
     @torch.inference_mode()
     def propose_eagle3_batch(self, seqs: list[Sequence]) -> list[list[int]]:
         """k greedy draft tokens per sequence (fewer near max_tokens) from the
-        recurrent states (model_runner.py:1159-1213).  Metadata for every
-        step goes to the device in one copy; the proposals come back in one."""
+        recurrent states (model_runner.py:1159-1213).  Draft step s consumes
+        the previous token at RoPE position len-1+s and writes its K/V at that
+        position's slot; every step's metadata goes to the device in one copy
+        and all proposals come back in one."""
         assert self.eagle3_model is not None
         k = self.speculative_config.num_speculative_tokens
         limits = [min(k, seq.max_tokens - seq.num_completion_tokens) for seq in seqs]
         steps = max(limits, default=0)
         if steps <= 0:
             return [[] for _ in seqs]
+        lens = [len(seq) for seq in seqs]
+        pos = [[n - 1 + s for n in lens] for s in range(steps - 1)]
+        slots = [[self._slot(seq, p) for seq, p in zip(seqs, row)] for row in pos]
+        ctx_lens = [[p + 1 for p in row] for row in pos]
+        state_rows = _pinned(self._state_rows(seqs), torch.int64).to(self.device, non_blocking=True)
+        bs = bucket_for(len(seqs))
+        if self._use_graphs() and steps == k and bs is not None:
+            graph = self._propose_graphs.get(bs)
+            if graph is None:
+                graph = self._propose_graphs[bs] = ProposeGraph(self, bs, k)
+            tokens = graph.run(state_rows, pos, slots, ctx_lens,
+                               [seq.block_table for seq in seqs])
+            table = tokens[:, :len(seqs)].cpu().tolist()
+        else:
+            table = self._propose_eager(seqs, state_rows, steps, pos, slots, ctx_lens, lens)
+        return [[table[s][i] for s in range(limits[i])] for i in range(len(seqs))]
+
+    def _propose_eager(self, seqs, state_rows, steps, pos, slots, ctx_lens, lens):
         try:
-            hidden = torch.cat([self.eagle3_states[s.seq_id].last_hidden_state for s in seqs])
-            feedback = torch.cat([self.eagle3_states[s.seq_id].last_feedback_hidden_state
-                                  for s in seqs])
+            hidden = self.state_hidden.index_select(0, state_rows)
+            feedback = self.state_feedback.index_select(0, state_rows)
             tokens = [self.eagle3_model.sample_greedy(hidden)]
             if steps > 1:
-                lens = [len(seq) for seq in seqs]
-                pos = [[n - 1 + s for n in lens] for s in range(steps - 1)]
-                slots = [[self._slot(seq, p) for seq, p in zip(seqs, row)] for row in pos]
-                ctx_lens = [[p + 1 for p in row] for row in pos]
                 pos_d = _pinned(pos, torch.int64).to(self.device, non_blocking=True)
                 slot_d = _pinned(slots, torch.int32).to(self.device, non_blocking=True)
                 ctx_d = _pinned(ctx_lens, torch.int32).to(self.device, non_blocking=True)
@@ -353,10 +417,23 @@ class ModelRunner:
                     hidden, feedback = self.eagle3_model.forward_with_cache(tokens[-1], pos_d[s],
                                                                             feedback)
                     tokens.append(self.eagle3_model.sample_greedy(hidden))
-            table = torch.stack(tokens).cpu().tolist()
-            return [[table[s][i] for s in range(limits[i])] for i in range(len(seqs))]
+            return torch.stack(tokens).cpu().tolist()
         finally:
             reset_context()
+
+    def _verify_metadata(self, seqs):
+        """Host lists of the verify window [num_computed, +scheduled) of every
+        sequence (the rows prepare_prefill builds)."""
+        ids, pos, slots, cu_q, cu_k = [], [], [], [0], [0]
+        for seq in seqs:
+            start = seq.num_computed_tokens
+            end = min(start + seq.num_scheduled_tokens, seq.num_tokens)
+            ids.extend(seq.token_ids[start:end])
+            pos.extend(range(start, end))
+            slots.extend(self._slot(seq, p) for p in range(start, end))
+            cu_q.append(cu_q[-1] + end - start)
+            cu_k.append(cu_k[-1] + end)
+        return ids, pos, slots, cu_q, cu_k
 
     @torch.inference_mode()
     def verify_eagle3_batch_fused(self, seqs: list[Sequence], num_input_tokens: list[int]):
@@ -366,30 +443,52 @@ class ModelRunner:
         pairs stay on the device for ``commit_eagle3_batch``."""
         if len(seqs) != len(num_input_tokens):
             raise ValueError("EAGLE3 verification metadata does not match requests")
+        k = self.speculative_config.num_speculative_tokens
+        b = len(seqs)
+        bs = bucket_for(b)
         try:
             for seq, n in zip(seqs, num_input_tokens):
                 seq.num_scheduled_tokens = n
-            input_ids, positions = self.prepare_prefill(seqs)
-            ctx = get_context()
-            hidden, aux = self.model.forward_with_aux_hidden_states(
-                input_ids, positions, self.speculative_config.aux_hidden_state_layers)
-            logits = self.model.compute_all_logits(hidden)
-            t, b = logits.shape[0], len(seqs)
-            n = t + 2 * b
-            if n > self._verify_dev.numel():
-                self._verify_dev = torch.empty(2 * n, dtype=torch.int32, device=self.device)
-                self._verify_host = torch.empty(2 * n, dtype=torch.int32, pin_memory=True)
-            K.argmax_accept(logits, ctx.cu_seqlens_q, input_ids, out=self._verify_dev[:n])
-            self._verify_host[:n].copy_(self._verify_dev[:n], non_blocking=True)
-            torch.cuda.current_stream().synchronize()
-            res = self._verify_host[:n].tolist()
-            _, cu = self._host_prefill
-            if self.keep_verify_inputs:
-                self.last_verify_inputs = (logits, list(cu), input_ids)
-            argmax = res[:t]
+            if (self._use_graphs() and self.use_verify_graph and bs is not None
+                    and not self.keep_verify_inputs
+                    and all(n == k + 1 for n in num_input_tokens)):
+                ids, pos, slots, cu, cu_k = self._verify_metadata(seqs)
+                graph = self._verify_graphs.get(bs)
+                if graph is None:
+                    graph = self._verify_graphs[bs] = VerifyGraph(self, bs, k + 1)
+                graph.run(ids, pos, cu, cu_k, slots, [seq.block_table for seq in seqs])
+                t_pad = graph.T
+                self._verify_host[:t_pad + 2 * bs].copy_(graph.out, non_blocking=True)
+                torch.cuda.current_stream().synchronize()
+                res = self._verify_host[:t_pad + 2 * bs].tolist()
+                argmax = res[:cu[-1]]
+                acc = res[t_pad:t_pad + b]
+                bonus = res[t_pad + bs:t_pad + bs + b]
+                aux = graph.aux
+                self._pending_graph = graph
+            else:
+                input_ids, positions = self.prepare_prefill(seqs)
+                ctx = get_context()
+                hidden, aux = self.model.forward_with_aux_hidden_states(
+                    input_ids, positions, self.speculative_config.aux_hidden_state_layers)
+                logits = self.model.compute_all_logits(hidden)
+                t = logits.shape[0]
+                n = t + 2 * b
+                if n > self._verify_dev.numel():
+                    self._verify_dev = torch.empty(2 * n, dtype=torch.int32, device=self.device)
+                    self._verify_host = torch.empty(2 * n, dtype=torch.int32, pin_memory=True)
+                K.argmax_accept(logits, ctx.cu_seqlens_q, input_ids, out=self._verify_dev[:n])
+                self._verify_host[:n].copy_(self._verify_dev[:n], non_blocking=True)
+                torch.cuda.current_stream().synchronize()
+                res = self._verify_host[:n].tolist()
+                _, cu = self._host_prefill
+                if self.keep_verify_inputs:
+                    self.last_verify_inputs = (logits, list(cu), input_ids)
+                argmax, acc, bonus = res[:t], res[t:t + b], res[t + b:n]
+                self._pending_graph = None
             targets = [argmax[cu[i]:cu[i + 1]] for i in range(b)]
             self._pending_verify = (aux, cu, {seq.seq_id: i for i, seq in enumerate(seqs)})
-            return targets, res[t:t + b], res[t + b:n]
+            return targets, acc, bonus
         finally:
             for seq in seqs:
                 seq.num_scheduled_tokens = 0
@@ -422,6 +521,24 @@ class ModelRunner:
                 raise RuntimeError("committed tail longer than the verify window")
             rows.extend(range(cu[i], cu[i] + len(toks)))
         if not rows:
+            return
+        lens = {len(t) for t in output_tokens}
+        graph = self._pending_graph
+        if graph is not None and len(lens) == 1 and len(seqs) <= graph.bs:
+            n = lens.pop()
+            key = (graph.bs, n)
+            cg = self._commit_graphs.get(key)
+            if cg is None:
+                cg = self._commit_graphs[key] = CommitGraph(self, graph, n)
+            ids, pos, slots, cq, ck = [], [], [], [0], [0]
+            for seq, toks, start in zip(seqs, output_tokens, start_positions):
+                ids.extend(toks)
+                pos.extend(range(start, start + n))
+                slots.extend(self._slot(seq, p) for p in range(start, start + n))
+                cq.append(cq[-1] + n)
+                ck.append(ck[-1] + start + n)
+            cg.run(rows, ids, pos, cq, ck, slots, [seq.block_table for seq in seqs])
+            self._store_states(seqs, cg.hidden, cg.feedback, [cq[i + 1] - 1 for i in range(len(seqs))])
             return
         rows_d = _pinned(rows, torch.int32).to(self.device, non_blocking=True)
         combined = self.eagle3_model.combine_hidden_states(aux_concat(aux, rows_d))
@@ -458,15 +575,14 @@ class ModelRunner:
             hidden, feedback = self.eagle3_model.forward_with_cache(
                 _pinned(ids, torch.int64).to(dev, non_blocking=True),
                 _pinned(pos, torch.int64).to(dev, non_blocking=True), combined)
-            for i, seq in enumerate(seqs):
-                r = cu_q[i + 1] - 1
-                self.eagle3_states[seq.seq_id] = Eagle3KVCache(hidden[r:r + 1].clone(),
-                                                               feedback[r:r + 1].clone())
+            self._store_states(seqs, hidden, feedback, [cu_q[i + 1] - 1 for i in range(len(seqs))])
         finally:
             reset_context()
 
     def release_eagle3_state(self, seq_id: int) -> None:
-        self.eagle3_states.pop(seq_id, None)
+        r = self._state_slot.pop(seq_id, None)
+        if r is not None:
+            self._free_state.append(r)
 
     @torch.inference_mode()
     def run_eagle3_graph(self, input_ids, positions, feedback, seqs):

@@ -29,10 +29,10 @@ def dirs(tmp_path_factory):
     return target, draft
 
 
-def make_llm(dirs, spec=True, k=4, blocks=96):
+def make_llm(dirs, spec=True, k=4, blocks=96, eager=True):
     target, draft = dirs
     kw = dict(load_format="dummy", seed=0, max_model_len=2048, num_kvcache_blocks=blocks,
-              enforce_eager=True, max_num_batched_tokens=4096)
+              enforce_eager=eager, max_num_batched_tokens=4096)
     if spec:
         kw["speculative_config"] = {"method": "eagle3", "model": draft,
                                     "num_speculative_tokens": k, "aux_hidden_state_layers": AUX}
@@ -179,3 +179,24 @@ def test_errors_match_reference(dirs):
             spec.add_request("text prompt", SamplingParams(temperature=0.0))
     finally:
         spec.exit()
+
+
+def test_hip_graph_steps_are_greedy(dirs):
+    """The captured verify / propose / commit graphs (padded buckets) produce
+    the same greedy paths as the eager engine."""
+    ps = prompts(6, seed=3)
+    sp = SamplingParams(temperature=0.0, max_tokens=33, ignore_eos=True)
+    eager = make_llm(dirs, spec=True, eager=True)
+    try:
+        ref = [o["token_ids"] for o in eager.generate(ps, sp, use_tqdm=False)]
+    finally:
+        eager.exit()
+    graphed = make_llm(dirs, spec=True, eager=False)
+    try:
+        got = [o["token_ids"] for o in graphed.generate(ps, sp, use_tqdm=False)]
+        caps = graphed.model_runner.get_eagle3_runtime_capabilities()
+        assert caps["cuda_graph"] and caps["graph_batch_sizes"]
+        for p, a, b in zip(ps, got, ref):
+            assert_same_greedy_path(graphed, p, a, b)
+    finally:
+        graphed.exit()
