@@ -1,12 +1,12 @@
 // K1: paged verify attention for gfx950 (MFMA 16x16x32 bf16).
 //
-// Work decomposition: one 256-thread workgroup (4 waves) per
-// (query tile, kv split, kv head, sequence).  A query tile is up to 64/G
-// consecutive query positions of one sequence times the G query heads that
-// share the kv head (G = Hq / Hkv), padded to NT*16 columns (NT = 1..4); a
-// verify step (k+1 positions, G <= 64/(k+1)) is a single tile, a prefill is
-// many.  Each tile only walks the keys its last row can see.  The key range of the split is walked in 32-key chunks,
-// chunk c by wave c % 4, each wave keeping its own online-softmax state.
+// Work decomposition: one wave (64 threads) per (query tile, kv split, kv
+// head, sequence).  A query tile is up to 64/G consecutive query positions of
+// one sequence times the G query heads that share the kv head (G = Hq / Hkv),
+// padded to NT*16 columns (NT = 1..4); a verify step (k+1 positions,
+// G <= 64/(k+1)) is a single tile, a prefill is many.  Each tile only walks
+// the keys its last row can see.  A split (768 keys by default) is walked in
+// 32-key chunks with one online-softmax state per query column.
 //
 // Per 32-key chunk a wave computes S^T = K . Q^T (two 16-key tiles, MFMA with
 // keys as M, query rows as N, head_dim as K in four 32-wide slices) and
@@ -22,10 +22,10 @@
 //     tile (row pitch 68 dwords: conflict-free for the column reads) and read
 //     back two head_dim elements per dword, feeding an even and an odd d-tile.
 // FP8 caches are dequantised to bf16 on load (exact: every e4m3 value is a
-// bf16 value).  The waves' states are merged through LDS at the end; a split
-// that covers the whole sequence writes bf16 output directly, otherwise it
-// writes a normalised fp32 partial plus its log-sum-exp, and a second kernel
-// merges the splits.
+// bf16 value).  At the end the wave transposes O^T through its LDS stage; a
+// split that covers the whole sequence writes bf16 output directly, otherwise
+// it writes a normalised fp32 partial plus its log-sum-exp, and a second
+// kernel merges the splits.
 #include <stdlib.h>
 
 #include "common.h"
@@ -129,10 +129,15 @@ __global__ void __launch_bounds__(kWave, NT >= 4 ? 1 : 2)
 paged_attention_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(16))) uint32_t vst[kVStage];
 
-  const int split = blockIdx.x % p.max_splits;
-  const int qt = blockIdx.x / p.max_splits;
-  const int kvh = blockIdx.y;
-  const int seq = blockIdx.z;
+  // Dispatch order (x fastest): kv head, sequence, then (query tile, split)
+  // slowest.  Every full split of every sequence is dispatched before the
+  // shorter trailing splits (longest work first), and the empty splits that
+  // pad the grid come last instead of recurring at fixed positions of the
+  // dispatch order, where they left a fixed subset of CUs idle.
+  const int kvh = blockIdx.x;
+  const int seq = blockIdx.y;
+  const int split = blockIdx.z % p.max_splits;
+  const int qt = blockIdx.z / p.max_splits;
   const int lane = threadIdx.x;
   const int g = lane >> 4;
   const int m16 = lane & 15;
@@ -556,7 +561,7 @@ int run_attention(AttnParams& p, int kv_dtype, void* workspace, size_t workspace
     p.ws_lse = nullptr;
   }
   const bool fp8 = kv_dtype == NVA_KV_FP8_E4M3;
-  dim3 grid(p.max_splits * p.n_qtiles, p.hkv, p.num_seqs);
+  dim3 grid(p.hkv, p.num_seqs, p.max_splits * p.n_qtiles);
   const int nt = (tile_rows + 15) / 16;
   if (nt <= 1)
     launch_nt<1>(p, fp8, grid, s);
