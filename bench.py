@@ -8,12 +8,13 @@ is accepted tok/s = tokens committed in the K timed steps / their wall time
 already prefilled (prefill is not timed).
 
 The same JSON line carries
-  roofline:      the verify attention kernel (K1), timed with HIP events on
-                 its stream around every verify-attention launch of
-                 --roofline-steps further steps of the same workload (the
-                 timed steps replay HIP graphs, inside which ROCm torch cannot
-                 record timing events, so these steps launch the verify
-                 forward eagerly); achieved = algorithmic bytes per launch /
+  roofline:      the verify attention call (K1: attention kernel + split
+                 combine), timed with HIP events on its stream: one further
+                 step of the same workload runs its verify forward eagerly
+                 (the timed steps replay HIP graphs, inside which ROCm torch
+                 cannot record timing events), and its 36 verify-attention
+                 launches are re-issued back to back --roofline-repeats times
+                 between two events; achieved = algorithmic bytes per launch /
                  mean launch time, algorithmic bytes = sum_i L_i*Hkv*D*2B*2
                  (K and V read once) + T*Hq*D*2B*2 (Q in, O out);
   cpu_baseline:  the reference's host acceptance logic (per-sequence bf16
@@ -35,6 +36,18 @@ sys.path.insert(0, os.path.join(ROOT, "extend-nano-vllm_amd"))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+
+# HBM bytes per verify-attention call (attention kernel + split combine) on
+# this workload, from two rocprofv3 --pmc runs of `bench.py --attention-only`
+# (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch, averaged over 363 calls),
+# scaled by what the same counters read for a 1 GiB device copy in the same
+# runs: FETCH_SIZE 524300 KiB (x2.0 to bytes read), WRITE_SIZE 1048576 KiB
+# (x1.0).  attention: FETCH 158720.7, WRITE 12687.1; combine: FETCH 6000.4,
+# WRITE 2496.0.  Only quoted for the default workload, whose shapes it was
+# measured on.
+PMC_TRAFFIC_BYTES = int(((158720.7 + 6000.4) * 2.0 + (12687.1 + 2496.0) * 1.0) * 1024)
+PMC_WORKLOAD = dict(preset="qwen3-8b", batch=64, k=5, prompt_min=256, prompt_max=2048,
+                    max_tokens=256, seed=2)
 METRIC = "accepted tok/s, Qwen3-8B EAGLE3 k=5 bs64; verify-attn HBM GB/s % of peak"
 
 
@@ -54,66 +67,83 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="bound on the CPU-baseline sample's run time")
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--roofline-steps", type=int, default=5,
-                    help="extra steps with the verify forward run eagerly so that every "
-                         "verify-attention launch is bracketed by HIP events")
+    ap.add_argument("--roofline-repeats", type=int, default=10,
+                    help="times the verify-attention launches of one step are re-issued "
+                         "between HIP events for the roofline figure")
+    ap.add_argument("--attention-only", action="store_true",
+                    help="run only the verify-attention launches of the workload and a "
+                         "1 GiB copy (for hardware-counter runs); prints their own JSON")
     return ap.parse_args()
 
 
 class AttnTimer:
-    """Brackets each verify-attention launch with HIP events on the current
-    stream (the stream the kernels are enqueued on) and records its
-    algorithmic bytes from the host-side metadata."""
+    """Times the verify-attention launches of one speculative step.
+
+    While ``capture`` is set, every verify-attention call made by the verify
+    forward (launched eagerly) is recorded with its arguments and its
+    algorithmic bytes, computed from the host-side metadata.  ``measure``
+    then re-issues those exact launches back to back, ``repeats`` times, on
+    the current stream (the one the kernels are enqueued on), between two HIP
+    events, so that the mean launch time is the kernels' own time and not the
+    host's launch latency.  The re-issued launches only read the K/V cache
+    and write fresh output buffers."""
 
     def __init__(self):
-        self.enabled = False
-        self.events = []
+        self.capture = False
+        self.calls = []
         self.bytes = []
+        self.current_lens = None
+        self.orig = None
 
     def wrap(self, kernels):
-        import torch
-
         orig = kernels.paged_attention_varlen
+        self.orig = orig
         timer = self
 
-        def timed(q, k_cache, v_cache, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
-                  softmax_scale, block_table, causal=True, k_scale=None, v_scale=None, out=None):
-            if not timer.enabled or timer.current_lens is None:
-                return orig(q, k_cache, v_cache, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
-                            max_seqlen_k, softmax_scale, block_table, causal, k_scale, v_scale, out)
-            s = torch.cuda.Event(enable_timing=True)
-            e = torch.cuda.Event(enable_timing=True)
-            s.record()
+        def recorded(q, k_cache, v_cache, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
+                     softmax_scale, block_table, causal=True, k_scale=None, v_scale=None, out=None):
             o = orig(q, k_cache, v_cache, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
                      softmax_scale, block_table, causal, k_scale, v_scale, out)
-            e.record()
-            hkv, d = k_cache.shape[2], k_cache.shape[3]
-            esz = k_cache.element_size()
-            kv = sum(timer.current_lens) * hkv * d * esz * 2
-            qo = q.shape[0] * q.shape[1] * d * 2 * 2
-            timer.events.append((s, e))
-            timer.bytes.append(kv + qo)
+            if timer.capture and timer.current_lens is not None:
+                hkv, d = k_cache.shape[2], k_cache.shape[3]
+                kv = sum(timer.current_lens) * hkv * d * k_cache.element_size() * 2
+                qo = q.shape[0] * q.shape[1] * d * 2 * 2
+                timer.calls.append((q, k_cache, v_cache, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
+                                    max_seqlen_k, softmax_scale, block_table, causal, k_scale,
+                                    v_scale))
+                timer.bytes.append(kv + qo)
             return o
 
-        self.current_lens = None
-        kernels.paged_attention_varlen = timed
+        kernels.paged_attention_varlen = recorded
         import nanovllm_amd.layers as layers
-        layers.K.paged_attention_varlen = timed
+        layers.K.paged_attention_varlen = recorded
 
-    def result(self):
+    def measure(self, repeats: int, traffic):
         import torch
 
-        torch.cuda.synchronize()
-        ms = [s.elapsed_time(e) for s, e in self.events]
-        if not ms:
+        if not self.calls:
             return None
-        mean_ms = sum(ms) / len(ms)
+        for args in self.calls:  # warm the workspace cache
+            self.orig(*args)
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record(stream)
+        for _ in range(repeats):
+            for args in self.calls:
+                self.orig(*args)
+        e.record(stream)
+        torch.cuda.synchronize()
+        launches = repeats * len(self.calls)
+        mean_ms = s.elapsed_time(e) / launches
         mean_bytes = sum(self.bytes) / len(self.bytes)
         gbs = mean_bytes / (mean_ms * 1e-3) / 1e9
+        self.calls = []
         return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "paged_attention_kernel (+ split combine)",
-                "launches": len(ms), "mean_us": round(mean_ms * 1e3, 2),
+                "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "kernel": "paged_attention_kernel + split combine_kernel (one verify-attention call)",
+                "launches": launches, "mean_us": round(mean_ms * 1e3, 2),
                 "bytes_per_launch": int(mean_bytes)}
 
 
@@ -154,6 +184,84 @@ def cpu_baseline(batches, seconds):
                       f"{model}; {total / len(times) * 1e3:.1f} ms per batch"}
 
 
+def attention_only(args) -> None:
+    """Verify attention alone on the bench workload's shapes, for counter runs.
+
+    The sequences are the bench's (same seeded prompt lengths) at the point
+    the roofline step verifies them: prompt + committed tokens + k+1 verify
+    rows, with random bf16 K/V in a cache whose block ids are shuffled.
+    Launches ``--roofline-repeats`` x 36 verify-attention calls (one step's
+    worth per repeat), then a plain device copy of 1 GiB as often, for
+    scaling FETCH_SIZE / WRITE_SIZE counter readings to bytes."""
+    import torch
+
+    from nanovllm_amd import kernels
+    from nanovllm_amd.synthetic import QWEN3_PRESETS
+
+    dev = torch.device("cuda", 0)
+    cfg = QWEN3_PRESETS[args.preset]
+    hq, hkv, d, layers = (cfg["num_attention_heads"], cfg["num_key_value_heads"], cfg["head_dim"],
+                          cfg["num_hidden_layers"])
+    g = torch.Generator().manual_seed(args.seed)
+    lens = torch.randint(args.prompt_min, args.prompt_max + 1, (args.batch,), generator=g).tolist()
+    done = args.warmup + args.steps + 2  # tokens each sequence holds when the roofline step runs
+    q_len = args.k + 1
+    seqlens = [L + done + q_len for L in lens]
+    block = 256
+    nblk = [-(-L // block) for L in seqlens]
+    total = sum(nblk)
+    perm = torch.randperm(total, generator=g)
+    width = max(nblk)
+    bt = torch.full((args.batch, width), -1, dtype=torch.int32)
+    off = 0
+    for i, n in enumerate(nblk):
+        bt[i, :n] = perm[off:off + n].to(torch.int32)
+        off += n
+    kc = torch.randn(total, block, hkv, d, generator=g).to(torch.bfloat16).to(dev)
+    vc = torch.randn(total, block, hkv, d, generator=g).to(torch.bfloat16).to(dev)
+    T = args.batch * q_len
+    q = torch.randn(T, hq, d, generator=g).to(torch.bfloat16).to(dev)
+    cu_q = torch.arange(0, T + 1, q_len, dtype=torch.int32).to(dev)
+    cu_k = torch.tensor([0] + seqlens, dtype=torch.int64).cumsum(0).to(torch.int32).to(dev)
+    bt = bt.to(dev)
+    out = torch.empty_like(q)
+    max_k = args.prompt_max + args.max_tokens + q_len  # the engine's max_seqlen_k
+    scale = d ** -0.5
+
+    def attn():
+        kernels.paged_attention_varlen(q, kc, vc, cu_q, cu_k, q_len, max_k, scale, bt, out=out)
+
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+    dst = torch.empty_like(src)
+
+    def timed(fn, n):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record(stream)
+        for _ in range(n):
+            fn()
+        e.record(stream)
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / n * 1e3
+
+    n_attn = args.roofline_repeats * layers
+    attn_us = timed(attn, n_attn)
+    copy_us = timed(lambda: dst.copy_(src), args.roofline_repeats)
+    byts = sum(seqlens) * hkv * d * 2 * 2 + T * hq * d * 2 * 2
+    print(json.dumps({"workload": "verify attention only", "batch": args.batch, "q_len": q_len,
+                      "sum_seqlen_k": sum(seqlens), "longest_seq": max(seqlens),
+                      "attention_calls": n_attn + 3, "attention_us": round(attn_us, 2),
+                      "bytes_per_call": byts,
+                      "achieved_GBs": round(byts / attn_us / 1e3, 1),
+                      "copy_bytes": src.numel(), "copy_calls": args.roofline_repeats + 3,
+                      "copy_us": round(copy_us, 1),
+                      "copy_GBs": round(2 * src.numel() / copy_us / 1e3, 1)}), flush=True)
+
+
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
@@ -164,6 +272,9 @@ def main():
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported by this build "
               "(single-GPU hot path; see DESIGN.md for how it would shard)", file=sys.stderr)
         sys.exit(2)
+    if args.attention_only:
+        attention_only(args)
+        return
     import torch
 
     from nanovllm_amd import LLM, SamplingParams
@@ -239,17 +350,17 @@ def main():
     elapsed = t1 - t0
     stats = {k: llm.spec_stats[k] - before[k] for k in before}
 
-    # roofline: the same workload for a few more steps with the verify forward
+    # roofline: one more step of the same workload with the verify forward
     # launched eagerly (events cannot be recorded inside a captured HIP graph
-    # on ROCm); the kernels and their inputs are those of the timed steps
+    # on ROCm); its verify-attention launches, with the timed steps' kernels
+    # and shapes, are then re-issued back to back between HIP events
     runner.use_verify_graph = False
-    timer.enabled = True
-    for _ in range(args.roofline_steps):
-        llm.step()
-    torch.cuda.synchronize()
-    timer.enabled = False
+    timer.capture = True
+    llm.step()
+    timer.capture = False
     runner.use_verify_graph = True
-    roof = timer.result()
+    default_workload = all(getattr(args, key) == val for key, val in PMC_WORKLOAD.items())
+    roof = timer.measure(args.roofline_repeats, PMC_TRAFFIC_BYTES if default_workload else None)
 
     log(f"timed {args.steps} steps in {elapsed:.3f}s")
     cpu = None
