@@ -1,0 +1,314 @@
+"""Host-side logic of the speculative step on the CPU: acceptance rule,
+speculation bookkeeping of Scheduler / BlockManager, decode metadata and the
+runner's graph-metadata copy.  Expected values are hand-worked from the
+reference's code or taken from its own tests (cited per test)."""
+import json
+import os
+import random
+from types import SimpleNamespace
+
+import pytest
+import torch
+
+from nanovllm_amd.engine import model_runner as mr
+from nanovllm_amd.engine.graphs import BUCKETS, bucket_for
+from nanovllm_amd.engine.scheduler import Scheduler
+from nanovllm_amd.engine.sequence import Sequence, SequenceStatus
+from nanovllm_amd.engine.speculative import verify_greedy_proposals
+from nanovllm_amd.context import get_context, reset_context, set_context
+from nanovllm_amd.sampling_params import SamplingParams
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+BS = 256
+
+
+# ---------------------------------------------------------------- acceptance rule
+
+def test_engine_acceptance_rule_on_golden_vectors():
+    """speculative.py:11-30 of the reference, through the engine's own symbol."""
+    cases = json.load(open(os.path.join(GOLDEN, "accept_cases.json")))["cases"]
+    for c in cases:
+        if "error" in c:
+            with pytest.raises(ValueError):
+                verify_greedy_proposals(c["proposal"], c["target"])
+            continue
+        v = verify_greedy_proposals(c["proposal"], c["target"])
+        assert v.accepted_count == c["accepted"]
+        assert v.accepted_tokens == c["tokens"]
+        assert v.replacement_token == c["replacement"]
+
+
+# ---------------------------------------------------------------- scheduler / blocks
+
+def _scheduler(num_blocks=16, k=5, eos=7, max_num_seqs=8):
+    cfg = SimpleNamespace(max_num_seqs=max_num_seqs, max_num_batched_tokens=1 << 16,
+                          enable_prefill_batching=True,
+                          speculative_config=SimpleNamespace(num_speculative_tokens=k),
+                          eos=eos, num_kvcache_blocks=num_blocks, kvcache_block_size=BS,
+                          enable_prefix_caching=True)
+    return Scheduler(cfg)
+
+
+def _prefilled(sched, prompt, first_token, **sp):
+    """Admit and prefill one sequence (scheduler.py prefill branch + postprocess)."""
+    seq = Sequence(list(prompt), SamplingParams(temperature=0.0, **sp))
+    sched.add(seq)
+    seqs, is_prefill = sched.schedule()
+    assert is_prefill and seqs == [seq]
+    sched.postprocess(seqs, [first_token], True)
+    return seq
+
+
+def _spec_step(sched, seq, proposal, target):
+    """One speculative step in the engine's order (llm_engine.py:124-178)."""
+    seqs, is_prefill = sched.schedule()
+    assert not is_prefill and seq in seqs
+    sched.reserve_speculation(seq)
+    base = sched.begin_speculation(seq, proposal)
+    seq.num_computed_tokens = base - 1
+    v = verify_greedy_proposals(proposal, target)
+    committed = sched.postprocess_speculation(seq, base, v.accepted_tokens, v.replacement_token)
+    return base, committed
+
+
+def _check_invariants(sched, live):
+    bm = sched.block_manager
+    assert len(bm.free_block_ids) + len(bm.used_block_ids) == len(bm.blocks)
+    refs = {}
+    for seq in live:
+        if seq.is_finished:
+            continue
+        assert len(seq.block_table) == seq.num_blocks
+        for b in seq.block_table:
+            refs[b] = refs.get(b, 0) + 1
+    assert set(refs) == bm.used_block_ids
+    for b, n in refs.items():
+        assert bm.blocks[b].ref_count == n
+
+
+def test_full_acceptance_across_a_page_boundary():
+    """250-token prompt: the five drafts fill page 0 exactly, the bonus opens
+    page 1 (scheduler.py:172-182 page finalisation)."""
+    sched = _scheduler()
+    seq = _prefilled(sched, range(100, 350), 1, max_tokens=64, ignore_eos=True)
+    assert len(seq) == 251 and len(seq.block_table) == 1
+    base, committed = _spec_step(sched, seq, [11, 12, 13, 14, 15], [11, 12, 13, 14, 15, 16])
+    assert (base, committed) == (251, 5)
+    assert seq.token_ids[250:] == [1, 11, 12, 13, 14, 15, 16]
+    assert len(seq) == 257 and len(seq.block_table) == 2
+    assert seq.num_computed_tokens == 256
+    first = sched.block_manager.blocks[seq.block_table[0]]
+    assert first.ready and first.hash != -1
+    _check_invariants(sched, [seq])
+
+
+def test_rejection_frees_the_reserved_page():
+    """254-token prompt: the reservation takes page 1 for the drafts; rejecting
+    all of them truncates it away (block_manager.py:197-205)."""
+    sched = _scheduler()
+    seq = _prefilled(sched, range(254), 1, max_tokens=64, ignore_eos=True)
+    seqs, _ = sched.schedule()
+    sched.reserve_speculation(seq)
+    assert len(seq.block_table) == 2                      # ceil((255 + 5) / 256)
+    reserved = seq.block_table[1]
+    base = sched.begin_speculation(seq, [5, 6, 7, 8, 9])
+    seq.num_computed_tokens = base - 1
+    v = verify_greedy_proposals([5, 6, 7, 8, 9], [4, 6, 7, 8, 9, 10])
+    assert sched.postprocess_speculation(seq, base, v.accepted_tokens, v.replacement_token) == 0
+    assert seq.token_ids[254:] == [1, 4] and len(seq) == 256
+    assert len(seq.block_table) == 1
+    assert reserved in sched.block_manager.free_block_ids
+    assert seq.num_computed_tokens == 255
+    _check_invariants(sched, [seq])
+
+
+def test_eos_inside_accepted_drafts_ends_the_sequence():
+    """EOS truncation drops the replacement and finishes (scheduler.py:158-163)."""
+    sched = _scheduler(eos=7)
+    seq = _prefilled(sched, range(10, 40), 1, max_tokens=64)
+    base, committed = _spec_step(sched, seq, [3, 7, 9, 9, 9], [3, 7, 9, 9, 9, 5])
+    assert committed == 2
+    assert seq.completion_token_ids == [1, 3, 7]
+    assert seq.status == SequenceStatus.FINISHED and not seq.block_table
+    assert not sched.running
+    assert len(sched.block_manager.free_block_ids) == 16
+
+
+def test_max_tokens_clips_the_accepted_drafts():
+    """Accepted drafts are clipped to the remaining budget, with no replacement
+    (scheduler.py:156-157)."""
+    sched = _scheduler()
+    seq = _prefilled(sched, range(30), 1, max_tokens=3, ignore_eos=True)
+    sched.schedule()
+    sched.reserve_speculation(seq)
+    # reserve covers min(prompt + max_tokens, len + k) = min(33, 36) tokens
+    assert len(seq.block_table) == 1
+    base = sched.begin_speculation(seq, [4, 5, 6])
+    v = verify_greedy_proposals([4, 5, 6], [4, 5, 6, 8])
+    assert sched.postprocess_speculation(seq, base, v.accepted_tokens, v.replacement_token) == 2
+    assert seq.completion_token_ids == [1, 4, 5]
+    assert seq.is_finished
+
+
+def test_replacement_only_when_budget_remains():
+    sched = _scheduler()
+    seq = _prefilled(sched, range(30), 1, max_tokens=2, ignore_eos=True)
+    base, committed = _spec_step(sched, seq, [4], [9, 9])
+    assert committed == 0
+    assert seq.completion_token_ids == [1, 9]
+    assert seq.is_finished
+
+
+def test_random_speculation_keeps_block_accounting_consistent():
+    """Many steps over several sequences with random acceptance: the block
+    table always covers ceil(len/256) pages, reference counts match the
+    tables, and freed pages return to the pool."""
+    rng = random.Random(0)
+    sched = _scheduler(num_blocks=64, k=5, eos=-1)
+    live = []
+    for i in range(4):
+        prompt = [rng.randrange(1000) for _ in range(rng.randrange(200, 700))]
+        live.append(Sequence(prompt, SamplingParams(temperature=0.0, max_tokens=300,
+                                                    ignore_eos=True)))
+        sched.add(live[-1])
+    seqs, is_prefill = sched.schedule()                   # prefill batching: all four
+    assert is_prefill and seqs == live
+    sched.postprocess(seqs, [rng.randrange(1000) for _ in seqs], True)
+    steps = 0
+    while sched.running and steps < 400:
+        seqs, is_prefill = sched.schedule()
+        assert not is_prefill
+        for seq in seqs:
+            sched.reserve_speculation(seq)
+            k = min(5, seq.max_tokens - seq.num_completion_tokens)
+            proposal = [rng.randrange(1000) for _ in range(k)]
+            a = rng.randrange(k + 1)
+            target = proposal[:a] + [rng.randrange(1000, 2000)] + \
+                [rng.randrange(1000) for _ in range(k - a)]
+            base = sched.begin_speculation(seq, proposal)
+            seq.num_computed_tokens = base - 1
+            before = seq.token_ids[:base]
+            v = verify_greedy_proposals(proposal, target)
+            assert v.accepted_count == a
+            c = sched.postprocess_speculation(seq, base, v.accepted_tokens, v.replacement_token)
+            assert seq.token_ids[:base] == before
+            assert seq.token_ids[base:base + c] == proposal[:c]
+            if not seq.is_finished:
+                assert seq.num_computed_tokens == base + c
+        _check_invariants(sched, live)
+        steps += 1
+    assert all(s.is_finished for s in live)
+    assert all(s.num_completion_tokens == 300 for s in live)
+    assert len(sched.block_manager.free_block_ids) == 64
+
+
+def test_prefix_cache_hash_is_chained_xxhash64():
+    """Block hashes chain the previous hash as 8 little-endian bytes before
+    the int64 token ids (block_manager.py compute_hash)."""
+    import numpy as np
+    import xxhash
+
+    from nanovllm_amd.engine.block_manager import BlockManager
+
+    toks = list(range(256))
+    h0 = xxhash.xxh64(np.array(toks, dtype=np.int64).tobytes()).intdigest()
+    assert BlockManager.compute_hash(toks) == h0
+    h1 = xxhash.xxh64(h0.to_bytes(8, "little") + np.array(toks, dtype=np.int64).tobytes())
+    assert BlockManager.compute_hash(toks, h0) == h1.intdigest()
+
+
+# ---------------------------------------------------------------- runner metadata
+
+@pytest.fixture
+def cpu_runner(monkeypatch):
+    monkeypatch.setattr(mr, "_pinned", lambda values, dtype: torch.tensor(values, dtype=dtype))
+    runner = mr.ModelRunner.__new__(mr.ModelRunner)
+    runner.block_size = BS
+    runner.device = torch.device("cpu")
+    yield runner
+    reset_context()
+
+
+def test_prepare_decode_slots_match_reference_vector(cpu_runner):
+    """tests/test_decode_context.py:26-32 of the reference."""
+    cpu_runner.prepare_block_tables = lambda seqs: torch.tensor(
+        [[seq.block_table[0]] for seq in seqs], dtype=torch.int32)
+    first = Sequence([11] * 16)
+    second = Sequence([12] * 17)
+    first.block_table = [3]
+    second.block_table = [5]
+    input_ids, positions = cpu_runner.prepare_decode([first, second])
+    ctx = get_context()
+    assert not ctx.is_prefill
+    assert input_ids.tolist() == [11, 12]
+    assert positions.tolist() == [15, 16]
+    assert ctx.context_lens.tolist() == [16, 17]
+    assert ctx.slot_mapping.tolist() == [3 * 256 + 15, 5 * 256 + 16]
+
+
+def test_runtime_capabilities(cpu_runner):
+    """tests/test_eagle3_runtime.py:24-50 of the reference."""
+    cpu_runner.eagle3_model = object()
+    cpu_runner.eagle_kv_cache = torch.empty(2, 1, 2, 4, 1, 8)
+    cpu_runner.eagle_graphs = {1: object()}
+    caps = cpu_runner.get_eagle3_runtime_capabilities()
+    assert caps["paged_kv_cache"] is True
+    assert caps["cuda_graph"] is True
+    assert caps["graph_batch_sizes"] == [1]
+    cpu_runner.eagle3_model = None
+    cpu_runner.eagle_kv_cache = None
+    cpu_runner.eagle_graphs = {}
+    cpu_runner._propose_graphs = {}
+    assert cpu_runner.get_eagle3_runtime_capabilities() == {
+        "paged_kv_cache": False, "cuda_graph": False, "graph_batch_sizes": []}
+
+
+def test_graph_replay_copies_paged_metadata(cpu_runner):
+    """tests/test_eagle3_runtime.py:53-91 of the reference."""
+    class FakeGraph:
+        def replay(self):
+            return None
+
+    cpu_runner.eagle_graphs = {1: FakeGraph()}
+    cpu_runner.eagle_graph_vars = {1: {
+        "input_ids": torch.zeros(1, dtype=torch.int64),
+        "positions": torch.zeros(1, dtype=torch.int64),
+        "feedback": torch.zeros(1, 2),
+        "slot_mapping": torch.full((1,), -1, dtype=torch.int32),
+        "context_lens": torch.ones(1, dtype=torch.int32),
+        "block_tables": torch.zeros(1, 2, dtype=torch.int32),
+        "outputs": (torch.ones(1, 2), torch.full((1, 2), 2.0)),
+    }}
+    set_context(False, slot_mapping=torch.tensor([7], dtype=torch.int32),
+                context_lens=torch.tensor([9], dtype=torch.int32),
+                block_tables=torch.tensor([[3, 4]], dtype=torch.int32))
+    hidden, feedback = cpu_runner.run_eagle3_graph(torch.tensor([5]), torch.tensor([8]),
+                                                   torch.zeros(1, 2), [object()])
+    v = cpu_runner.eagle_graph_vars[1]
+    assert v["slot_mapping"].tolist() == [7]
+    assert v["context_lens"].tolist() == [9]
+    assert v["block_tables"].tolist() == [[3, 4]]
+    assert hidden.tolist() == [[1.0, 1.0]]
+    assert feedback.tolist() == [[2.0, 2.0]]
+
+
+def test_bucket_for_picks_the_smallest_covering_bucket():
+    assert bucket_for(1) == 1
+    assert bucket_for(3) == 4
+    assert bucket_for(64) == 64
+    assert bucket_for(65) == 96
+    assert bucket_for(BUCKETS[-1]) == BUCKETS[-1]
+    assert bucket_for(BUCKETS[-1] + 1) is None
+
+
+def test_config_rejects_multi_gpu_and_bad_kv_dtype(tmp_path):
+    from nanovllm_amd.config import Config
+    from nanovllm_amd.synthetic import write_qwen3_config
+
+    path = write_qwen3_config(str(tmp_path / "m"), "tiny")
+    with pytest.raises(ValueError, match="one GPU"):
+        Config(path, tensor_parallel_size=2)
+    with pytest.raises(ValueError, match="kv_cache_dtype"):
+        Config(path, kv_cache_dtype="int8")
+    with pytest.raises(ValueError):
+        Config(str(tmp_path / "missing"))
