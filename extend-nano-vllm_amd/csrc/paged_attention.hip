@@ -1,12 +1,21 @@
 // K1: paged verify attention for gfx950 (MFMA 16x16x32 bf16).
 //
-// Work decomposition: one wave (64 threads) per (query tile, kv split, kv
-// head, sequence).  A query tile is up to 64/G consecutive query positions of
-// one sequence times the G query heads that share the kv head (G = Hq / Hkv),
-// padded to NT*16 columns (NT = 1..4); a verify step (k+1 positions,
-// G <= 64/(k+1)) is a single tile, a prefill is many.  Each tile only walks
-// the keys its last row can see.  A split (768 keys by default) is walked in
-// 32-key chunks with one online-softmax state per query column.
+// Unit of work: one wave (64 threads) runs a *segment* -- one query tile of
+// one sequence against a contiguous key range, for one kv head.  A query
+// tile is up to 64/G consecutive query positions of a sequence times the G
+// query heads that share the kv head (G = Hq / Hkv), padded to NT*16 columns
+// (NT = 1, 2, 4); a verify step (k+1 positions) is a single tile, a prefill
+// is many.  Each tile only walks the keys its last row can see.  Segments
+// come from one of two decompositions:
+//   * stream (single-tile sequences of at most 16 rows, bf16 cache): per kv
+//     head the key chunks of all sequences are laid end to end and cut into
+//     one equal range per SIMD of the device, so every wave streams the same
+//     number of keys whatever the length mix;
+//   * fixed (everything else): one wave per (kv head, sequence, query tile,
+//     768-key split), several resident per SIMD.
+// A sequence covered by one segment gets bf16 output directly; otherwise
+// each segment writes a normalised fp32 partial plus its log-sum-exp and
+// combine_kernel merges them.
 //
 // Per 32-key chunk a wave computes S^T = K . Q^T (two 16-key tiles, MFMA with
 // keys as M, query rows as N, head_dim as K in four 32-wide slices) and
@@ -14,18 +23,22 @@
 //   * The MFMA sums over K in any order, so K and Q operands only have to
 //     agree on which head_dim element sits in which lane slot: lane l holds
 //     row (l % 16) and elements 32*s + 8*(l/16) .. +7 of slice s, a 16-byte
-//     load straight from the paged cache.
+//     load straight from the paged cache.  The Q operands are parked in LDS
+//     in that order and re-read per chunk, so they hold no registers.
 //   * The S^T accumulator layout (lane l: query column l % 16, keys
 //     4*(l/16) + i) is exactly the B-operand layout of the P^T operand once
 //     the 8 lane slots are mapped to keys {4g..4g+3, 16+4g..16+4g+3}; V^T uses
 //     the same key mapping.  V is therefore staged through a wave-private LDS
 //     tile (row pitch 68 dwords: conflict-free for the column reads) and read
 //     back two head_dim elements per dword, feeding an even and an odd d-tile.
+//   * K/V loads are raw buffer loads from a per-chunk descriptor (uniform
+//     base, loop-invariant lane offsets, record count ending at the last
+//     visible key so that rows past it read as zeros).  Where a SIMD holds
+//     a single wave (64-row tiles) or dequantisation lengthens the math
+//     (FP8), they are issued one chunk ahead into a second register buffer.
 // FP8 caches are dequantised to bf16 on load (exact: every e4m3 value is a
-// bf16 value).  At the end the wave transposes O^T through its LDS stage; a
-// split that covers the whole sequence writes bf16 output directly, otherwise
-// it writes a normalised fp32 partial plus its log-sum-exp, and a second
-// kernel merges the splits.
+// bf16 value).  At the end the wave transposes O^T through its LDS stage and
+// writes 16-byte rows.
 #include <stdlib.h>
 
 #include "common.h"
@@ -44,6 +57,8 @@ static_assert(16 * kAccPitch + 16 <= kVStage, "output tile must fit the V stage"
 constexpr int kSplitKeys = 768;
 constexpr int kMinSplit = 128;
 constexpr int64_t kMinWorkgroups = 1024;
+constexpr int kMaxSeqGroups = 8;        // stream mode: up to 8 * 64 sequences
+constexpr int kMinRangeChunks = 4;      // stream mode: at least 128 keys per range
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kRescaleSlack = 8.0f;   // log2 headroom before the running max moves
 
@@ -74,9 +89,20 @@ struct AttnParams {
   float* ws_lse;
   int32_t split_len, max_splits;
   int32_t qtile, n_qtiles;                            // query positions per workgroup
+  // stream decomposition (one query tile per sequence)
+  int32_t min_range_chunks, max_range_chunks;
+  int32_t* seq_nsplit;                                // [num_seqs] split counts for the combine
 };
 
 __device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Raw buffer descriptor over num_records bytes at base: loads at offsets
+// past the end return zeros (dword 3: 32-bit data format, no swizzle).
+constexpr int kRsrcWord3 = 0x00020000;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int num_records) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), num_records,
+                                           kRsrcWord3);
+}
 
 // Orders a wave's own LDS writes and reads: LDS executes one wave's
 // operations in issue order, so the compiler must only keep program order
@@ -122,51 +148,28 @@ __device__ __forceinline__ void seq_geometry(const AttnParams& p, int seq, int& 
   L = L > p.max_k ? p.max_k : L;
 }
 
-// two waves per SIMD fit the register budget of tiles up to 32 columns;
-// 64-column tiles (NT = 4) need the full register file of one wave
-template <int NT, bool FP8>
-__global__ void __launch_bounds__(kWave, NT >= 4 ? 1 : 2)
-paged_attention_kernel(AttnParams p) {
-  __shared__ __attribute__((aligned(16))) uint32_t vst[kVStage];
-
-  // Dispatch order (x fastest): kv head, sequence, then (query tile, split)
-  // slowest.  Every full split of every sequence is dispatched before the
-  // shorter trailing splits (longest work first), and the empty splits that
-  // pad the grid come last instead of recurring at fixed positions of the
-  // dispatch order, where they left a fixed subset of CUs idle.
-  const int kvh = blockIdx.x;
-  const int seq = blockIdx.y;
-  const int split = blockIdx.z % p.max_splits;
-  const int qt = blockIdx.z / p.max_splits;
+// One segment of work: the query tile qt of sequence seq (all its rows
+// for kv head kvh) against keys [kv_begin, kv_end), which is split `split`
+// of the `nsplit` splits covering the keys the tile can see.  A single split
+// writes the bf16 output; otherwise a normalised fp32 partial and its
+// log-sum-exp go to the workspace for combine_kernel.
+template <int NT, bool FP8, bool PIPE>
+__device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vst, bf16x8_t* qst,
+                                               const int kvh, const int seq, const int qt,
+                                               const int kv_begin, const int kv_end,
+                                               const int split, const int nsplit) {
   const int lane = threadIdx.x;
   const int g = lane >> 4;
   const int m16 = lane & 15;
 
   int q_start, q_len, L;
   seq_geometry(p, seq, q_start, q_len, L);
-  // this workgroup's query positions: j0 .. j0 + jn - 1 of the sequence
+  // this tile's query positions: j0 .. j0 + jn - 1 of the sequence
   const int j0 = qt * p.qtile;
   const int jn = (q_len - j0 < p.qtile) ? q_len - j0 : p.qtile;
-  if (jn <= 0) return;
   const int rows = jn * p.group;
   // keys any row of the tile can see (bottom-right causal)
   const int kv_limit = L - q_len + j0 + jn;
-  const int kv_begin = split * p.split_len;
-  if (kv_limit <= 0) {
-    // nothing visible: zero output rows (once, from split 0)
-    if (split != 0) return;
-    for (int idx = lane; idx < rows * (kD / 8); idx += kWave) {
-      const int n = idx / (kD / 8), dv = idx % (kD / 8);
-      const int j = j0 + n / p.group, hh = n % p.group;
-      uint16_t* o = p.out + static_cast<int64_t>(q_start + j) * p.out_row_stride +
-                    static_cast<int64_t>(kvh * p.group + hh) * p.out_head_stride + dv * 8;
-      *reinterpret_cast<uint4*>(o) = make_uint4(0, 0, 0, 0);
-    }
-    return;
-  }
-  if (kv_begin >= kv_limit) return;
-  const int kv_end = kv_begin + p.split_len < kv_limit ? kv_begin + p.split_len : kv_limit;
-  const int nsplit = (kv_limit + p.split_len - 1) / p.split_len;
 
   float kscale = 1.0f, vscale = 1.0f;
   if (FP8) {
@@ -175,26 +178,31 @@ paged_attention_kernel(AttnParams p) {
   }
   const float sl2 = p.scale_log2 * kscale;
 
-  // ---- query operands and causal limits for this lane's columns
-  bf16x8_t qop[NT][4];
+  // ---- query operands (kept in LDS in operand order: entry (nt, s) is
+  // one 16-byte vector per lane, read back conflict-free for every chunk so
+  // that they hold no registers across the loop) and causal limits
   int lim[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const int n = nt * 16 + m16;
+    bf16x8_t qv[4];
     if (n < rows) {
       const int j = j0 + n / p.group, hh = n % p.group;
       const uint16_t* qp = p.q + static_cast<int64_t>(q_start + j) * p.q_row_stride +
                            static_cast<int64_t>(kvh * p.group + hh) * p.q_head_stride;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) qop[nt][s] = *reinterpret_cast<const bf16x8_t*>(qp + 32 * s + 8 * g);
+      for (int s = 0; s < 4; ++s) qv[s] = *reinterpret_cast<const bf16x8_t*>(qp + 32 * s + 8 * g);
       const int c = L - q_len + j;
       lim[nt] = c < L - 1 ? c : L - 1;
     } else {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) qop[nt][s] = bf16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
+      for (int s = 0; s < 4; ++s) qv[s] = bf16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
       lim[nt] = -1;
     }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qst[(nt * 4 + s) * kWave + lane] = qv[s];
   }
+  lds_wave_sync();
 
   float m_run[NT], l_run[NT];
   f32x4_t acc[NT][8];
@@ -211,78 +219,112 @@ paged_attention_kernel(AttnParams p) {
   constexpr int64_t esz = FP8 ? 1 : 2;
 
   // Block ids of this split, one per lane (lane i holds logical block
-  // first_blk + i): one load up front instead of a dependent load per chunk.
+  // first_blk + i; a split spans at most kWave blocks): one load up front
+  // instead of a dependent load per chunk.
   const int first_blk = kv_begin / p.block_size;
   const int nblk = (kv_end - 1) / p.block_size - first_blk + 1;
   int lane_blk = -1;
   if (lane < nblk && first_blk + lane < p.bt_cols) lane_blk = bt[first_blk + lane];
 
-  for (int c = 0; c < nchunks; ++c) {
-    const int kb = kv_begin + c * kChunk;
-    const int lb = kb / p.block_size;
-    int pblk = (lb - first_blk < kWave) ? __builtin_amdgcn_readlane(lane_blk, lb - first_blk)
-                                        : (lb < p.bt_cols ? bt[lb] : -1);
-    if (pblk < 0 || pblk >= p.num_blocks) continue;   // invalid block: keys masked
-    const int off0 = kb % p.block_size;
-    const int64_t blk_base = static_cast<int64_t>(pblk) * p.blk_stride +
-                             static_cast<int64_t>(kvh) * p.head_stride;
+  // Raw K/V registers of one 32-key chunk (bf16: K 2x4 and V 8 16-byte
+  // vectors per lane; FP8: K 2x4 8-byte and V 4 16-byte vectors).
+  struct Chunk {
+    uint4 k[2][4];
+    uint4 v[8];
+    int kb;        // first key of the chunk
+    bool valid;    // block id in range; otherwise the chunk's keys are masked
+  };
 
-    // ---- K operands straight from the cache: key (16*kt + m16), d 32*s + 8*g .. +7
-    uint4 kraw[2][4];
+  // Loop-invariant byte offsets of this lane's loads inside one (block, kv
+  // head) tile of 32 tokens; a chunk only builds two buffer descriptors
+  // (uniform), so no per-chunk address arithmetic runs on the vector ALUs.
+  //   K: key (16*kt + m16), d 32*s + 8*g .. +7   (s through the immediate offset)
+  //   V: bf16 row (4*i + g), d 8*m16 .. +7; FP8 row (8*i + lane/8), bytes 16*(lane%8)
+  const uint32_t tokb = static_cast<uint32_t>(p.tok_stride * esz);
+  uint32_t koff[2], voff[8];
+#pragma unroll
+  for (int kt = 0; kt < 2; ++kt) koff[kt] = (kt * 16 + m16) * tokb + 8 * g * esz;
+#pragma unroll
+  for (int i = 0; i < 8; ++i)
+    voff[i] = FP8 ? (8 * i + (lane >> 3)) * tokb + (lane & 7) * 16 : (4 * i + g) * tokb + m16 * 16;
+
+  // Issue the loads of chunk c (no waits: the data is consumed by
+  // compute_chunk one chunk later, so each load's latency overlaps the
+  // previous chunk's math).  The descriptors' record count ends at the last
+  // visible key, so rows past the sequence end (and every row of an invalid
+  // block) read as zeros instead of stale cache contents.
+  auto load_chunk = [&](int c, Chunk& ch) {
+    const int kb = kv_begin + c * kChunk;
+    ch.kb = kb;
+    // the host keeps a split within kWave blocks, so the id is always in a lane
+    const int raw = __builtin_amdgcn_readlane(lane_blk, kb / p.block_size - first_blk);
+    ch.valid = raw >= 0 && raw < p.num_blocks;
+    const int pblk = ch.valid ? raw : 0;
+    const int visible = kv_limit - kb < kChunk ? kv_limit - kb : kChunk;
+    const int nrec = ch.valid ? visible * static_cast<int>(tokb) : 0;
+    const int64_t tile = (static_cast<int64_t>(pblk) * p.blk_stride +
+                          static_cast<int64_t>(kvh) * p.head_stride +
+                          static_cast<int64_t>(kb % p.block_size) * p.tok_stride) * esz;
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(p.k_cache + tile, nrec);
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(p.v_cache + tile, nrec);
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
-      int key = kb + kt * 16 + m16;
-      key = key < kv_limit ? key : kv_limit - 1;
-      const int64_t e = blk_base + static_cast<int64_t>(off0 + key - kb) * p.tok_stride;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         if (FP8) {
-          const uint2 w = *reinterpret_cast<const uint2*>(p.k_cache + (e + 32 * s + 8 * g));
-          kraw[kt][s] = make_uint4(w.x, w.y, 0, 0);
+          const uint2 w = __builtin_bit_cast(
+              uint2, __builtin_amdgcn_raw_buffer_load_b64(kr, koff[kt] + 32 * s, 0, 0));
+          ch.k[kt][s] = make_uint4(w.x, w.y, 0, 0);
         } else {
-          kraw[kt][s] = *reinterpret_cast<const uint4*>(p.k_cache + (e + 32 * s + 8 * g) * esz);
+          ch.k[kt][s] = __builtin_bit_cast(
+              uint4, __builtin_amdgcn_raw_buffer_load_b128(kr, koff[kt] + 64 * s, 0, 0));
         }
       }
     }
-    // ---- V rows (coalesced) into the wave's LDS stage
+#pragma unroll
+    for (int i = 0; i < (FP8 ? 4 : 8); ++i)
+      ch.v[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(vr, voff[i], 0, 0));
+  };
+
+  auto compute_chunk = [&](const Chunk& ch) {
+    if (!ch.valid) return;
+    const int kb = ch.kb;
+    // ---- V rows into the wave's LDS stage.  The stage belongs to this wave
+    // alone and LDS executes a wave's operations in order, so a compiler
+    // barrier plus an LDS wait (before the first read) orders them.
     if (FP8) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = 8 * i + (lane >> 3);
-        int key = kb + row;
-        key = key < kv_limit ? key : kv_limit - 1;
-        const int64_t e = blk_base + static_cast<int64_t>(off0 + key - kb) * p.tok_stride + (lane & 7) * 16;
-        const uint4 w = *reinterpret_cast<const uint4*>(p.v_cache + e);
         uint32_t* dst = vst + row * kVPitch + (lane & 7) * 8;
-        *reinterpret_cast<bf16x8_t*>(dst) = fp8x8_to_bf16(make_uint2(w.x, w.y));
-        *reinterpret_cast<bf16x8_t*>(dst + 4) = fp8x8_to_bf16(make_uint2(w.z, w.w));
+        *reinterpret_cast<bf16x8_t*>(dst) = fp8x8_to_bf16(make_uint2(ch.v[i].x, ch.v[i].y));
+        *reinterpret_cast<bf16x8_t*>(dst + 4) = fp8x8_to_bf16(make_uint2(ch.v[i].z, ch.v[i].w));
       }
     } else {
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        int key = kb + 4 * i + g;
-        key = key < kv_limit ? key : kv_limit - 1;
-        const int64_t e = blk_base + static_cast<int64_t>(off0 + key - kb) * p.tok_stride + m16 * 8;
-        *reinterpret_cast<uint4*>(vst + (4 * i + g) * kVPitch + m16 * 4) =
-            *reinterpret_cast<const uint4*>(p.v_cache + e * esz);
-      }
+      for (int i = 0; i < 8; ++i)
+        *reinterpret_cast<uint4*>(vst + (4 * i + g) * kVPitch + m16 * 4) = ch.v[i];
     }
 
-    // ---- S^T = K . Q^T
+    // ---- S^T = K . Q^T: per head_dim slice s, every (key tile, query
+    // tile) pair; the query operands come from LDS one slice at a time
     f32x4_t sacc[2][NT];
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt) {
-      bf16x8_t kop[4];
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-        kop[s] = FP8 ? fp8x8_to_bf16(make_uint2(kraw[kt][s].x, kraw[kt][s].y))
-                     : __builtin_bit_cast(bf16x8_t, kraw[kt][s]);
+      for (int nt = 0; nt < NT; ++nt) sacc[kt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      bf16x8_t kop[2];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+        kop[kt] = FP8 ? fp8x8_to_bf16(make_uint2(ch.k[kt][s].x, ch.k[kt][s].y))
+                      : __builtin_bit_cast(bf16x8_t, ch.k[kt][s]);
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
-        f32x4_t a = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        const bf16x8_t qo = qst[(nt * 4 + s) * kWave + lane];
 #pragma unroll
-        for (int s = 0; s < 4; ++s) a = mfma(kop[s], qop[nt][s], a);
-        sacc[kt][nt] = a;
+        for (int kt = 0; kt < 2; ++kt) sacc[kt][nt] = mfma(kop[kt], qo, sacc[kt][nt]);
       }
     }
 
@@ -340,8 +382,6 @@ paged_attention_kernel(AttnParams p) {
       pb[nt] = __builtin_bit_cast(bf16x8_t, pk);
     }
 
-    // the stage was written by this wave only: LDS executes a wave's
-    // operations in order, so a compiler barrier plus an LDS wait suffices
     lds_wave_sync();
 
     // ---- O^T += V^T . P^T ; pair pp covers d = 32*pp + 2*m + {0 (even tile), 1 (odd tile)}
@@ -372,6 +412,35 @@ paged_attention_kernel(AttnParams p) {
     }
     // the next chunk overwrites the stage: its reads must be done first
     lds_wave_sync();
+  };
+
+  // Two register buffers, unrolled by two so that no buffer is copied: the
+  // loads of chunk c+1 are issued before chunk c is computed.  The
+  // scheduling barriers keep the compiler from sinking them to their use.
+  // Every load is unconditional (past the end the last chunk is loaded
+  // again, from L2) so the compiler's wait counts only ever wait for the
+  // older buffer.
+  if constexpr (PIPE) {
+    Chunk ca, cb;
+    load_chunk(0, ca);
+    const int last = nchunks - 1;
+    int c = 0;
+    for (; c < last; c += 2) {
+      load_chunk(c + 1, cb);
+      __builtin_amdgcn_sched_barrier(0);
+      compute_chunk(ca);
+      load_chunk(c + 2 < last ? c + 2 : last, ca);
+      __builtin_amdgcn_sched_barrier(0);
+      compute_chunk(cb);
+    }
+    if (c == last) compute_chunk(ca);
+  } else {
+    // one buffer: a second resident wave on the SIMD hides the latency
+    Chunk ca;
+    for (int c = 0; c < nchunks; ++c) {
+      load_chunk(c, ca);
+      compute_chunk(ca);
+    }
   }
 
   // ---- finish: per column sum, transpose O^T through LDS, 16-byte stores.
@@ -436,6 +505,142 @@ paged_attention_kernel(AttnParams p) {
   }
 }
 
+// zero the output rows of a query tile that sees no keys
+__device__ __forceinline__ void zero_tile(const AttnParams& p, int kvh, int seq, int qt) {
+  int q_start, q_len, L;
+  seq_geometry(p, seq, q_start, q_len, L);
+  const int j0 = qt * p.qtile;
+  const int jn = (q_len - j0 < p.qtile) ? q_len - j0 : p.qtile;
+  for (int idx = threadIdx.x; idx < jn * p.group * (kD / 8); idx += kWave) {
+    const int n = idx / (kD / 8), dv = idx % (kD / 8);
+    const int j = j0 + n / p.group, hh = n % p.group;
+    uint16_t* o = p.out + static_cast<int64_t>(q_start + j) * p.out_row_stride +
+                  static_cast<int64_t>(kvh * p.group + hh) * p.out_head_stride + dv * 8;
+    *reinterpret_cast<uint4*>(o) = make_uint4(0, 0, 0, 0);
+  }
+}
+
+// keys the single query tile of a sequence sees, in 32-key chunks (stream mode)
+__device__ __forceinline__ int stream_chunks(const AttnParams& p, int seq) {
+  int q_start, q_len, L;
+  seq_geometry(p, seq, q_start, q_len, L);
+  return (q_len > 0 && L > 0) ? (L + kChunk - 1) / kChunk : 0;
+}
+
+// Fixed decomposition, one wave per (kv head, sequence, query tile, split):
+// used when a sequence has several query tiles (prefill).
+// Dispatch order (x fastest): kv head, sequence, then (query tile, split)
+// slowest, so every full split is dispatched before the shorter trailing
+// splits and the empty splits that pad the grid come last.
+// Two waves per SIMD fit the register budget of tiles up to 32 columns;
+// 64-column tiles (NT = 4) need the full register file of one wave.
+template <int NT, bool FP8, bool PIPE>
+__global__ void __launch_bounds__(kWave, NT >= 4 ? 1 : 2)
+paged_attention_kernel(AttnParams p) {
+  __shared__ __attribute__((aligned(16))) uint32_t vst[kVStage];
+  __shared__ bf16x8_t qst[NT * 4 * kWave];
+  const int kvh = blockIdx.x;
+  const int seq = blockIdx.y;
+  const int split = blockIdx.z % p.max_splits;
+  const int qt = blockIdx.z / p.max_splits;
+  int q_start, q_len, L;
+  seq_geometry(p, seq, q_start, q_len, L);
+  const int j0 = qt * p.qtile;
+  const int jn = (q_len - j0 < p.qtile) ? q_len - j0 : p.qtile;
+  if (jn <= 0) return;
+  const int kv_limit = L - q_len + j0 + jn;
+  if (kv_limit <= 0) {
+    if (split == 0) zero_tile(p, kvh, seq, qt);
+    return;
+  }
+  const int kv_begin = split * p.split_len;
+  if (kv_begin >= kv_limit) return;
+  const int kv_end = kv_begin + p.split_len < kv_limit ? kv_begin + p.split_len : kv_limit;
+  const int nsplit = (kv_limit + p.split_len - 1) / p.split_len;
+  attend_segment<NT, FP8, PIPE>(p, vst, qst, kvh, seq, qt, kv_begin, kv_end, split, nsplit);
+}
+
+// Balanced ("stream") decomposition for one query tile per sequence (verify
+// and decode).  For each kv head, the chunks of all sequences are laid end
+// to end and cut into equal ranges of rc chunks; workgroup (kvh, r) takes
+// ranges r, r + gridDim.y, ...  A range may cover the tail of one sequence
+// and the head of the next, so every workgroup streams the same number of
+// keys whatever the length mix, and no wave waits behind a long sequence.
+// Sequence s's split index is its range index minus that of its first chunk.
+template <int NT, bool FP8, bool PIPE>
+__global__ void __launch_bounds__(kWave, PIPE ? 1 : 2)
+paged_attention_stream_kernel(AttnParams p) {
+  __shared__ __attribute__((aligned(16))) uint32_t vst[kVStage];
+  __shared__ bf16x8_t qst[NT * 4 * kWave];
+  __shared__ int pre[kMaxSeqGroups * kWave + 1];          // pre[s]: chunks of sequences < s
+  const int kvh = blockIdx.x;
+  const int lane = threadIdx.x;
+
+  // exclusive prefix of the per-sequence chunk counts, one 64-sequence group
+  // at a time (wave-wide inclusive scan plus the running carry)
+  int carry = 0;
+  if (lane == 0) pre[0] = 0;
+  for (int base = 0; base < p.num_seqs; base += kWave) {
+    int v = base + lane < p.num_seqs ? stream_chunks(p, base + lane) : 0;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+      const int u = __shfl_up(v, d, kWave);
+      if (lane >= d) v += u;
+    }
+    if (base + lane < p.num_seqs) pre[base + lane + 1] = carry + v;
+    carry += __shfl(v, kWave - 1, kWave);
+  }
+  lds_wave_sync();
+  const int total = carry;
+  auto incl_of = [&](int s) { return pre[s + 1]; };
+  const int rc_even = (total + static_cast<int>(gridDim.y) - 1) / static_cast<int>(gridDim.y);
+  int rc = rc_even > p.min_range_chunks ? rc_even : p.min_range_chunks;
+  rc = rc < p.max_range_chunks ? rc : p.max_range_chunks;
+
+  if (blockIdx.y == 0) {
+    for (int s = 0; s < p.num_seqs; ++s) {
+      const int hi = incl_of(s);
+      const int lo = s > 0 ? incl_of(s - 1) : 0;
+      const int ns = hi > lo ? (hi - 1) / rc - lo / rc + 1 : 0;
+      if (hi == lo) {
+        int q_start, q_len, L;
+        seq_geometry(p, s, q_start, q_len, L);
+        if (q_len > 0) zero_tile(p, kvh, s, 0);
+      }
+      // split count per sequence for combine_kernel (one writer)
+      if (kvh == 0 && lane == 0 && p.seq_nsplit) p.seq_nsplit[s] = ns;
+    }
+  }
+
+  for (int r = blockIdx.y; r * rc < total; r += gridDim.y) {
+    const int start = r * rc;
+    const int end = start + rc < total ? start + rc : total;
+    // first sequence whose chunks reach past `start` (binary search on the
+    // monotone prefix)
+    int s = 0, hi_s = p.num_seqs - 1;
+    while (s < hi_s) {
+      const int mid = (s + hi_s) >> 1;
+      if (pre[mid + 1] <= start) s = mid + 1; else hi_s = mid;
+    }
+    for (; s < p.num_seqs; ++s) {
+      const int hi = incl_of(s);
+      const int lo = s > 0 ? incl_of(s - 1) : 0;
+      if (lo >= end) break;
+      if (hi <= start) continue;
+      const int c0 = (start > lo ? start : lo) - lo;
+      const int c1 = (end < hi ? end : hi) - lo;
+      int q_start, q_len, L;
+      seq_geometry(p, s, q_start, q_len, L);
+      const int kv_limit = L;
+      const int kv_begin = c0 * kChunk;
+      const int kv_end = c1 * kChunk < kv_limit ? c1 * kChunk : kv_limit;
+      const int split = r - lo / rc;
+      const int nsplit = (hi - 1) / rc - lo / rc + 1;
+      attend_segment<NT, FP8, PIPE>(p, vst, qst, kvh, s, 0, kv_begin, kv_end, split, nsplit);
+    }
+  }
+}
+
 // Merge split partials: one wave per (token row, q head); lane covers 2 d.
 __global__ void __launch_bounds__(kCombineThreads)
 combine_kernel(AttnParams p) {
@@ -460,10 +665,15 @@ combine_kernel(AttnParams p) {
   const int j = t - q_start;
   if (j >= q_len) return;
   // the split count of this row's query tile (same rule as the main kernel)
-  const int j0 = j / p.qtile * p.qtile;
-  const int jn = (q_len - j0 < p.qtile) ? q_len - j0 : p.qtile;
-  const int kv_limit = L - q_len + j0 + jn;
-  const int nsplit = kv_limit > 0 ? (kv_limit + p.split_len - 1) / p.split_len : 0;
+  int nsplit;
+  if (p.seq_nsplit) {
+    nsplit = p.seq_nsplit[seq];
+  } else {
+    const int j0 = j / p.qtile * p.qtile;
+    const int jn = (q_len - j0 < p.qtile) ? q_len - j0 : p.qtile;
+    const int kv_limit = L - q_len + j0 + jn;
+    nsplit = kv_limit > 0 ? (kv_limit + p.split_len - 1) / p.split_len : 0;
+  }
   if (nsplit <= 1) return;
   const int64_t base = (static_cast<int64_t>(t) * p.hq + h) * p.max_splits;
   float M = -INFINITY;
@@ -511,23 +721,103 @@ void choose_split(int32_t num_seqs, int32_t num_kv_heads, int32_t n_qtiles, int3
   *max_splits = (mk + len - 1) / len;
 }
 
+// Stream decomposition applies when every sequence is a single query tile
+// of at most 32 rows (64-row tiles need the whole register file for the
+// fixed decomposition's state already).
+// Decomposition and pipelining per tile shape, from measurements on MI355X
+// (Qwen3-0.6B/8B/32B verify and draft-decode shapes):
+//   * single-tile sequences of up to 16 rows, bf16: stream decomposition, one
+//     wave per SIMD, one chunk buffer;
+//   * up to 32 rows, bf16: fixed decomposition, one chunk buffer, three waves
+//     per SIMD hide each other's latency;
+//   * 64-row tiles and FP8: fixed decomposition with the chunk loads issued
+//     one chunk ahead (one wave per SIMD for 64 rows: no room for a second).
+// NVA_ATTN_STREAM=0/1 and NVA_ATTN_PIPE=0/1 override the choices (tuning).
+int env_choice(const char* name) {
+  const char* v = getenv(name);
+  return v ? (atoi(v) != 0) : -1;
+}
+
+bool stream_mode(int32_t num_seqs, int32_t max_q, int32_t qtile, int32_t group, bool fp8) {
+  static const int forced = env_choice("NVA_ATTN_STREAM");
+  if (forced == 0 || fp8 || max_q > qtile || num_seqs > kMaxSeqGroups * kWave) return false;
+  return forced == 1 ? max_q * group <= 32 : max_q * group <= 16;
+}
+
+bool pipelined(int nt, bool fp8) {
+  static const int forced = env_choice("NVA_ATTN_PIPE");
+  return forced >= 0 ? forced == 1 : (nt >= 4 || fp8);
+}
+
+// Upper bound on a sequence's split count in stream mode: a range holds at
+// least kMinRangeChunks chunks, and a sequence may start mid-range.
+int32_t stream_max_splits(int32_t max_k) {
+  const int32_t chunks = (max_k + kChunk - 1) / kChunk;
+  return (chunks + kMinRangeChunks - 1) / kMinRangeChunks + 1;
+}
+
+// Stream workgroups per kv head: one wave per SIMD of the device (cached).
+int32_t stream_ranges_per_head(int32_t hkv) {
+  static int32_t simds[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (simds[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+      cus = 256;
+    int per_simd = 1;
+    if (const char* v = getenv("NVA_ATTN_STREAM_WAVES")) per_simd = atoi(v) > 0 ? atoi(v) : 1;
+    simds[dev] = cus * 4 * per_simd;
+  }
+  const int32_t h = hkv > 0 ? hkv : 1;
+  return (simds[dev] + h - 1) / h;
+}
+
+// Workspace for either KV dtype (the size query does not name one): the
+// larger of the stream and fixed layouts that could apply.
 size_t workspace_bytes(int32_t num_seqs, int32_t num_tokens, int32_t hq, int32_t hkv, int32_t max_q,
                        int32_t max_k) {
   const int32_t qtile = choose_qtile(max_q, hkv > 0 ? hq / hkv : 1);
+  size_t bytes = 0;
+  if (stream_mode(num_seqs, max_q, qtile, hkv > 0 ? hq / hkv : 1, false)) {
+    const size_t slots = static_cast<size_t>(num_tokens) * hq * stream_max_splits(max_k);
+    bytes = slots * kD * sizeof(float) + slots * sizeof(float) +
+            static_cast<size_t>(num_seqs) * sizeof(int32_t) + 512;
+  }
   const int32_t n_qtiles = (max_q + qtile - 1) / qtile;
   int32_t len, ms;
   choose_split(num_seqs, hkv, n_qtiles, max_k, &len, &ms);
-  if (ms <= 1) return 0;
-  const size_t slots = static_cast<size_t>(num_tokens) * hq * ms;
-  return slots * kD * sizeof(float) + slots * sizeof(float) + 256;
+  if (ms > 1) {
+    const size_t slots = static_cast<size_t>(num_tokens) * hq * ms;
+    const size_t fixed = slots * kD * sizeof(float) + slots * sizeof(float) + 256;
+    bytes = fixed > bytes ? fixed : bytes;
+  }
+  return bytes;
 }
 
 template <int NT>
-void launch_nt(const AttnParams& p, bool fp8, dim3 grid, hipStream_t s) {
-  if (fp8)
-    paged_attention_kernel<NT, true><<<grid, kWave, 0, s>>>(p);
-  else
-    paged_attention_kernel<NT, false><<<grid, kWave, 0, s>>>(p);
+void launch_nt(const AttnParams& p, bool fp8, bool stream, dim3 grid, hipStream_t s) {
+  const bool pipe = pipelined(NT, fp8);
+  if constexpr (NT < 4) {
+    if (stream) {
+      if (pipe)
+        paged_attention_stream_kernel<NT, false, true><<<grid, kWave, 0, s>>>(p);
+      else
+        paged_attention_stream_kernel<NT, false, false><<<grid, kWave, 0, s>>>(p);
+      return;
+    }
+  }
+  if (pipe) {
+    if (fp8)
+      paged_attention_kernel<NT, true, true><<<grid, kWave, 0, s>>>(p);
+    else
+      paged_attention_kernel<NT, false, true><<<grid, kWave, 0, s>>>(p);
+  } else {
+    if (fp8)
+      paged_attention_kernel<NT, true, false><<<grid, kWave, 0, s>>>(p);
+    else
+      paged_attention_kernel<NT, false, false><<<grid, kWave, 0, s>>>(p);
+  }
 }
 
 int run_attention(AttnParams& p, int kv_dtype, void* workspace, size_t workspace_bytes_, hipStream_t s) {
@@ -549,28 +839,43 @@ int run_attention(AttnParams& p, int kv_dtype, void* workspace, size_t workspace
       p.q_row_stride % 8 || p.q_head_stride % 8 || p.out_row_stride % 8 || p.out_head_stride % 8 ||
       p.blk_stride % vec_elems || p.tok_stride % vec_elems || p.head_stride % vec_elems)
     return NVA_ERR_UNSUPPORTED;
-  choose_split(p.num_seqs, p.hkv, p.n_qtiles, p.max_k, &p.split_len, &p.max_splits);
-  if (p.max_splits > 1) {
+  const bool fp8 = kv_dtype == NVA_KV_FP8_E4M3;
+  const bool stream = stream_mode(p.num_seqs, p.max_q, p.qtile, p.group, fp8);
+  dim3 grid;
+  p.seq_nsplit = nullptr;
+  if (stream) {
+    // a range may span at most kWave - 2 whole blocks (one block id per lane)
+    p.min_range_chunks = kMinRangeChunks;
+    p.max_range_chunks = (kWave - 2) * p.block_size / kChunk;
+    p.max_splits = stream_max_splits(p.max_k);
+    p.split_len = 0;
+    grid = dim3(p.hkv, stream_ranges_per_head(p.hkv), 1);
+  } else {
+    choose_split(p.num_seqs, p.hkv, p.n_qtiles, p.max_k, &p.split_len, &p.max_splits);
+    // the kernel keeps one block id per lane: a split may touch at most kWave blocks
+    if (p.split_len / p.block_size + 2 > kWave) return NVA_ERR_UNSUPPORTED;
+    grid = dim3(p.hkv, p.num_seqs, p.max_splits * p.n_qtiles);
+  }
+  if (stream || p.max_splits > 1) {
     const size_t need = workspace_bytes(p.num_seqs, p.num_tokens, p.hq, p.hkv, p.max_q, p.max_k);
     if (!workspace || workspace_bytes_ < need || !aligned16(workspace)) return NVA_ERR_WORKSPACE;
     const size_t slots = static_cast<size_t>(p.num_tokens) * p.hq * p.max_splits;
     p.ws_o = static_cast<float*>(workspace);
     p.ws_lse = p.ws_o + slots * kD;
+    if (stream) p.seq_nsplit = reinterpret_cast<int32_t*>(p.ws_lse + slots);
   } else {
     p.ws_o = nullptr;
     p.ws_lse = nullptr;
   }
-  const bool fp8 = kv_dtype == NVA_KV_FP8_E4M3;
-  dim3 grid(p.hkv, p.num_seqs, p.max_splits * p.n_qtiles);
   const int nt = (tile_rows + 15) / 16;
   if (nt <= 1)
-    launch_nt<1>(p, fp8, grid, s);
+    launch_nt<1>(p, fp8, stream, grid, s);
   else if (nt == 2)
-    launch_nt<2>(p, fp8, grid, s);
+    launch_nt<2>(p, fp8, stream, grid, s);
   else
-    launch_nt<4>(p, fp8, grid, s);
+    launch_nt<4>(p, fp8, stream, grid, s);
   if (hipGetLastError() != hipSuccess) return NVA_ERR_LAUNCH;
-  if (p.max_splits > 1) {
+  if (stream || p.max_splits > 1) {
     dim3 cgrid(p.num_tokens, (p.hq + kCombineWaves - 1) / kCombineWaves);
     combine_kernel<<<cgrid, kCombineThreads, 0, s>>>(p);
   }
