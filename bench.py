@@ -36,6 +36,8 @@ sys.path.insert(0, os.path.join(ROOT, "extend-nano-vllm_amd"))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
+DEFAULT_GEMM_TUNING = os.path.join(ROOT, "extend-nano-vllm_amd", "nanovllm_amd", "tuning",
+                                   "gemm_mi355x_qwen3_8b_eagle3.csv")
 
 # HBM bytes per verify-attention call (attention kernel + split combine) on
 # this workload, from two rocprofv3 --pmc runs of `bench.py --attention-only`
@@ -70,6 +72,8 @@ def parse_args():
     ap.add_argument("--roofline-repeats", type=int, default=10,
                     help="times the verify-attention launches of one step are re-issued "
                          "between HIP events for the roofline figure")
+    ap.add_argument("--gemm-tuning", default=DEFAULT_GEMM_TUNING,
+                    help="TunableOp results for the projection GEMMs ('' for library defaults)")
     ap.add_argument("--attention-only", action="store_true",
                     help="run only the verify-attention launches of the workload and a "
                          "1 GiB copy (for hardware-counter runs); prints their own JSON")
@@ -294,6 +298,7 @@ def main():
               max_model_len=max_len, num_kvcache_blocks=args.batch * blocks_per_seq + 8,
               max_num_batched_tokens=16384, enable_prefill_batching=True,
               enforce_eager=args.eager,
+              gemm_tuning_file=(args.gemm_tuning or None) if args.preset == "qwen3-8b" else None,
               speculative_config={"method": "eagle3", "model": draft,
                                   "num_speculative_tokens": args.k,
                                   "aux_hidden_state_layers": aux})
@@ -387,7 +392,8 @@ def main():
                    "preset": args.preset, "batch": args.batch, "k": args.k,
                    "prompt_len": [args.prompt_min, args.prompt_max],
                    "max_tokens": args.max_tokens, "active_seqs": n_active,
-                   "hip_graphs": not args.eager},
+                   "hip_graphs": not args.eager,
+                   "gemm_tuning": os.path.basename(args.gemm_tuning) if args.gemm_tuning else None},
         "roofline": roof,
         "cpu_baseline": cpu,
         "committed_tokens": committed,

@@ -55,6 +55,9 @@ class Config:
     quantization: str | None = None
     load_format: str = "auto"
     seed: int = 0
+    # PyTorch TunableOp results (CSV) naming the hipBLASLt / rocBLAS solution
+    # for each projection GEMM shape; looked up only, never tuned at run time
+    gemm_tuning_file: str | None = None
 
     def __post_init__(self):
         if not os.path.isdir(self.model):
@@ -73,6 +76,8 @@ class Config:
             raise ValueError("max_num_batched_tokens and max_num_seqs must be positive")
         if not 0.0 < self.gpu_memory_utilization <= 1.0:
             raise ValueError("gpu_memory_utilization must be in (0, 1]")
+        if self.gemm_tuning_file is not None and not os.path.isfile(self.gemm_tuning_file):
+            raise ValueError(f"gemm_tuning_file does not exist: {self.gemm_tuning_file}")
         if isinstance(self.speculative_config, dict):
             self.speculative_config = SpeculativeConfig(**self.speculative_config)
         if self.speculative_config is not None:

@@ -33,6 +33,20 @@ from nanovllm_amd.loader import load_model
 from nanovllm_amd.qwen3 import Qwen3ForCausalLM, aux_concat
 
 
+def _use_gemm_tuning(path: str) -> None:
+    """Dispatch the projection GEMMs through the solutions recorded in
+    ``path`` (PyTorch TunableOp results for this GPU and library versions).
+    Lookup only: no tuning runs, so HIP graph capture is unaffected; shapes
+    not in the file keep the library's default choice."""
+    import torch.cuda.tunable as tunable
+
+    tunable.enable(True)
+    tunable.tuning_enable(False)
+    tunable.record_untuned_enable(False)
+    if not tunable.read_file(path):
+        raise RuntimeError(f"cannot read GEMM tuning results {path}")
+
+
 def _pinned(values, dtype) -> torch.Tensor:
     return torch.tensor(values, dtype=dtype, pin_memory=True)
 
@@ -50,6 +64,8 @@ class ModelRunner:
         self.rank = rank
         self.device = torch.device("cuda", config.device_offset)
         torch.cuda.set_device(self.device)
+        if config.gemm_tuning_file is not None:
+            _use_gemm_tuning(config.gemm_tuning_file)
         self._exited = False
         self.decode_graph_replay_count = 0
         default_dtype = torch.get_default_dtype()

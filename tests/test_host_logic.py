@@ -312,3 +312,28 @@ def test_config_rejects_multi_gpu_and_bad_kv_dtype(tmp_path):
         Config(path, kv_cache_dtype="int8")
     with pytest.raises(ValueError):
         Config(str(tmp_path / "missing"))
+
+
+def test_gemm_tuning_file_is_well_formed(tmp_path):
+    """The packaged TunableOp results name one solution per projection GEMM
+    shape of the Qwen3-8B EAGLE3 step, and Config rejects a missing file."""
+    import csv
+
+    from nanovllm_amd.config import Config
+    from nanovllm_amd.synthetic import write_qwen3_config
+
+    path = os.path.join(os.path.dirname(__file__), "..", "extend-nano-vllm_amd", "nanovllm_amd",
+                        "tuning", "gemm_mi355x_qwen3_8b_eagle3.csv")
+    rows = list(csv.reader(open(path)))
+    validators = {r[1] for r in rows if r[0] == "Validator"}
+    assert {"PT_VERSION", "GCN_ARCH_NAME", "HIPBLASLT_VERSION"} <= validators
+    gemms = [r for r in rows if r[0].startswith("GemmTunableOp")]
+    shapes = {r[1].split("_ld_")[0] for r in gemms}
+    assert len(shapes) == len(gemms)                 # one solution per shape
+    # verify (384 rows) and draft (64 rows) projections of the 8B geometry
+    for shape in ("tn_6144_384_4096", "tn_4096_384_4096", "tn_24576_384_4096",
+                  "tn_4096_384_12288", "tn_151936_64_4096"):
+        assert shape in shapes
+    model = write_qwen3_config(str(tmp_path / "m"), "tiny")
+    with pytest.raises(ValueError, match="gemm_tuning_file"):
+        Config(model, gemm_tuning_file=str(tmp_path / "missing.csv"))
