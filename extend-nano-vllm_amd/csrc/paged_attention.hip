@@ -91,7 +91,7 @@ struct AttnParams {
   int32_t qtile, n_qtiles;                            // query positions per workgroup
   // stream decomposition (one query tile per sequence)
   int32_t min_range_chunks, max_range_chunks;
-  int32_t* seq_nsplit;                                // [num_seqs] split counts for the combine
+  int32_t* row_nsplit;                                // [num_tokens] split count per query row
 };
 
 __device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -520,6 +520,16 @@ __device__ __forceinline__ void zero_tile(const AttnParams& p, int kvh, int seq,
   }
 }
 
+// record the split count of a query tile's rows for combine_kernel (one
+// writer per tile: the kv-head-0 workgroup that also owns split 0)
+__device__ __forceinline__ void note_rows(const AttnParams& p, int seq, int qt, int nsplit) {
+  int q_start, q_len, L;
+  seq_geometry(p, seq, q_start, q_len, L);
+  const int j0 = qt * p.qtile;
+  const int jn = (q_len - j0 < p.qtile) ? q_len - j0 : p.qtile;
+  for (int j = threadIdx.x; j < jn; j += kWave) p.row_nsplit[q_start + j0 + j] = nsplit;
+}
+
 // keys the single query tile of a sequence sees, in 32-key chunks (stream mode)
 __device__ __forceinline__ int stream_chunks(const AttnParams& p, int seq) {
   int q_start, q_len, L;
@@ -549,6 +559,8 @@ paged_attention_kernel(AttnParams p) {
   const int jn = (q_len - j0 < p.qtile) ? q_len - j0 : p.qtile;
   if (jn <= 0) return;
   const int kv_limit = L - q_len + j0 + jn;
+  const int nsplit = kv_limit > 0 ? (kv_limit + p.split_len - 1) / p.split_len : 0;
+  if (kvh == 0 && split == 0 && p.row_nsplit) note_rows(p, seq, qt, nsplit);
   if (kv_limit <= 0) {
     if (split == 0) zero_tile(p, kvh, seq, qt);
     return;
@@ -556,7 +568,6 @@ paged_attention_kernel(AttnParams p) {
   const int kv_begin = split * p.split_len;
   if (kv_begin >= kv_limit) return;
   const int kv_end = kv_begin + p.split_len < kv_limit ? kv_begin + p.split_len : kv_limit;
-  const int nsplit = (kv_limit + p.split_len - 1) / p.split_len;
   attend_segment<NT, FP8, PIPE>(p, vst, qst, kvh, seq, qt, kv_begin, kv_end, split, nsplit);
 }
 
@@ -598,17 +609,23 @@ paged_attention_stream_kernel(AttnParams p) {
   rc = rc < p.max_range_chunks ? rc : p.max_range_chunks;
 
   if (blockIdx.y == 0) {
-    for (int s = 0; s < p.num_seqs; ++s) {
-      const int hi = incl_of(s);
-      const int lo = s > 0 ? incl_of(s - 1) : 0;
-      const int ns = hi > lo ? (hi - 1) / rc - lo / rc + 1 : 0;
-      if (hi == lo) {
+    // split count of every row for combine_kernel (one writer: kv head 0),
+    // one sequence per lane
+    if (kvh == 0 && p.row_nsplit) {
+      for (int s = lane; s < p.num_seqs; s += kWave) {
+        const int hi = pre[s + 1], lo = pre[s];
+        const int ns = hi > lo ? (hi - 1) / rc - lo / rc + 1 : 0;
         int q_start, q_len, L;
         seq_geometry(p, s, q_start, q_len, L);
-        if (q_len > 0) zero_tile(p, kvh, s, 0);
+        for (int j = 0; j < q_len; ++j) p.row_nsplit[q_start + j] = ns;
       }
-      // split count per sequence for combine_kernel (one writer)
-      if (kvh == 0 && lane == 0 && p.seq_nsplit) p.seq_nsplit[s] = ns;
+    }
+    // sequences with no visible key get zero rows
+    for (int s = 0; s < p.num_seqs; ++s) {
+      if (pre[s + 1] != pre[s]) continue;
+      int q_start, q_len, L;
+      seq_geometry(p, s, q_start, q_len, L);
+      if (q_len > 0) zero_tile(p, kvh, s, 0);
     }
   }
 
@@ -641,56 +658,59 @@ paged_attention_stream_kernel(AttnParams p) {
   }
 }
 
-// Merge split partials: one wave per (token row, q head); lane covers 2 d.
+// Merge split partials.  Workgroup (t, y) merges, for token row t, the
+// 256 (head, 4-element) slices y*256 .. of the row; each thread owns one
+// slice.  The attention kernel recorded each row's split count, so a row
+// costs one dependent load before its partials; every thread issues the
+// loads of up to kCombineBatch splits at once (partials are laid out
+// [row][head][split][d]) and merges batches with a running log-sum-exp.
+constexpr int kCombineBatch = 8;
 __global__ void __launch_bounds__(kCombineThreads)
 combine_kernel(AttnParams p) {
   const int t = blockIdx.x;
-  const int h = blockIdx.y * kCombineWaves + threadIdx.x / kWave;
-  const int lane = threadIdx.x & (kWave - 1);
-  if (h >= p.hq || t >= p.num_tokens) return;
-  int seq;
-  if (p.cu_q) {
-    if (t < p.cu_q[0] || t >= p.cu_q[p.num_seqs]) return;
-    int lo = 0, hi = p.num_seqs;
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (p.cu_q[mid] <= t) lo = mid; else hi = mid;
-    }
-    seq = lo;
-  } else {
-    seq = t;
-  }
-  int q_start, q_len, L;
-  seq_geometry(p, seq, q_start, q_len, L);
-  const int j = t - q_start;
-  if (j >= q_len) return;
-  // the split count of this row's query tile (same rule as the main kernel)
-  int nsplit;
-  if (p.seq_nsplit) {
-    nsplit = p.seq_nsplit[seq];
-  } else {
-    const int j0 = j / p.qtile * p.qtile;
-    const int jn = (q_len - j0 < p.qtile) ? q_len - j0 : p.qtile;
-    const int kv_limit = L - q_len + j0 + jn;
-    nsplit = kv_limit > 0 ? (kv_limit + p.split_len - 1) / p.split_len : 0;
-  }
-  if (nsplit <= 1) return;
+  const int tid = threadIdx.x;
+  if (t >= p.num_tokens) return;
+  // rows outside the batch's query range were not written by this call
+  const int lo = p.cu_q ? p.cu_q[0] : 0;
+  const int hi = p.cu_q ? p.cu_q[p.num_seqs] : p.num_seqs;
+  int nsplit = p.row_nsplit[t];
+  if (t < lo || t >= hi || nsplit <= 1) return;
+  nsplit = nsplit < p.max_splits ? nsplit : p.max_splits;
+  const int idx = blockIdx.y * kCombineThreads + tid;
+  if (idx >= p.hq * (kD / 4)) return;
+  const int h = idx / (kD / 4), d4 = idx % (kD / 4);
   const int64_t base = (static_cast<int64_t>(t) * p.hq + h) * p.max_splits;
-  float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, p.ws_lse[base + s]);
-  float wsum = 0.0f, o0 = 0.0f, o1 = 0.0f;
-  for (int s = 0; s < nsplit; ++s) {
-    const float lse = p.ws_lse[base + s];
-    const float w = (lse == -INFINITY) ? 0.0f : exp2f_fast(lse - M);
-    const float2 v = *reinterpret_cast<const float2*>(p.ws_o + (base + s) * kD + 2 * lane);
-    wsum += w;
-    o0 += w * v.x;
-    o1 += w * v.y;
+  float M = -INFINITY, wsum = 0.0f;
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s0 = 0; s0 < nsplit; s0 += kCombineBatch) {
+    float lse[kCombineBatch];
+    float4 v[kCombineBatch];
+#pragma unroll
+    for (int u = 0; u < kCombineBatch; ++u) {
+      const bool in = s0 + u < nsplit;
+      lse[u] = in ? p.ws_lse[base + s0 + u] : -INFINITY;
+      v[u] = in ? *reinterpret_cast<const float4*>(p.ws_o + (base + s0 + u) * kD + 4 * d4)
+                : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float mb = M;
+#pragma unroll
+    for (int u = 0; u < kCombineBatch; ++u) mb = fmaxf(mb, lse[u]);
+    if (mb == -INFINITY) continue;
+    const float r = M == -INFINITY ? 0.0f : exp2f_fast(M - mb);
+    wsum *= r;
+    o.x *= r; o.y *= r; o.z *= r; o.w *= r;
+#pragma unroll
+    for (int u = 0; u < kCombineBatch; ++u) {
+      const float w = lse[u] == -INFINITY ? 0.0f : exp2f_fast(lse[u] - mb);
+      wsum += w;
+      o.x += w * v[u].x; o.y += w * v[u].y; o.z += w * v[u].z; o.w += w * v[u].w;
+    }
+    M = mb;
   }
   const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
   uint16_t* op = p.out + static_cast<int64_t>(t) * p.out_row_stride +
-                 static_cast<int64_t>(h) * p.out_head_stride + 2 * lane;
-  *reinterpret_cast<uint32_t*>(op) = pack_bf16(o0 * inv, o1 * inv);
+                 static_cast<int64_t>(h) * p.out_head_stride + 4 * d4;
+  *reinterpret_cast<uint2*>(op) = make_uint2(pack_bf16(o.x * inv, o.y * inv), pack_bf16(o.z * inv, o.w * inv));
 }
 
 // query positions per workgroup: as many as fit 64 tile rows (>= 1)
@@ -782,14 +802,15 @@ size_t workspace_bytes(int32_t num_seqs, int32_t num_tokens, int32_t hq, int32_t
   if (stream_mode(num_seqs, max_q, qtile, hkv > 0 ? hq / hkv : 1, false)) {
     const size_t slots = static_cast<size_t>(num_tokens) * hq * stream_max_splits(max_k);
     bytes = slots * kD * sizeof(float) + slots * sizeof(float) +
-            static_cast<size_t>(num_seqs) * sizeof(int32_t) + 512;
+            static_cast<size_t>(num_tokens) * sizeof(int32_t) + 512;
   }
   const int32_t n_qtiles = (max_q + qtile - 1) / qtile;
   int32_t len, ms;
   choose_split(num_seqs, hkv, n_qtiles, max_k, &len, &ms);
   if (ms > 1) {
     const size_t slots = static_cast<size_t>(num_tokens) * hq * ms;
-    const size_t fixed = slots * kD * sizeof(float) + slots * sizeof(float) + 256;
+    const size_t fixed = slots * kD * sizeof(float) + slots * sizeof(float) +
+                         static_cast<size_t>(num_tokens) * sizeof(int32_t) + 256;
     bytes = fixed > bytes ? fixed : bytes;
   }
   return bytes;
@@ -842,7 +863,7 @@ int run_attention(AttnParams& p, int kv_dtype, void* workspace, size_t workspace
   const bool fp8 = kv_dtype == NVA_KV_FP8_E4M3;
   const bool stream = stream_mode(p.num_seqs, p.max_q, p.qtile, p.group, fp8);
   dim3 grid;
-  p.seq_nsplit = nullptr;
+  p.row_nsplit = nullptr;
   if (stream) {
     // a range may span at most kWave - 2 whole blocks (one block id per lane)
     p.min_range_chunks = kMinRangeChunks;
@@ -862,7 +883,7 @@ int run_attention(AttnParams& p, int kv_dtype, void* workspace, size_t workspace
     const size_t slots = static_cast<size_t>(p.num_tokens) * p.hq * p.max_splits;
     p.ws_o = static_cast<float*>(workspace);
     p.ws_lse = p.ws_o + slots * kD;
-    if (stream) p.seq_nsplit = reinterpret_cast<int32_t*>(p.ws_lse + slots);
+    p.row_nsplit = reinterpret_cast<int32_t*>(p.ws_lse + slots);
   } else {
     p.ws_o = nullptr;
     p.ws_lse = nullptr;
@@ -876,8 +897,9 @@ int run_attention(AttnParams& p, int kv_dtype, void* workspace, size_t workspace
     launch_nt<4>(p, fp8, stream, grid, s);
   if (hipGetLastError() != hipSuccess) return NVA_ERR_LAUNCH;
   if (stream || p.max_splits > 1) {
-    dim3 cgrid(p.num_tokens, (p.hq + kCombineWaves - 1) / kCombineWaves);
-    combine_kernel<<<cgrid, kCombineThreads, 0, s>>>(p);
+    const int slices = p.hq * (kD / 4);
+    combine_kernel<<<dim3(p.num_tokens, (slices + kCombineThreads - 1) / kCombineThreads),
+                     kCombineThreads, 0, s>>>(p);
   }
   return launch_status();
 }
