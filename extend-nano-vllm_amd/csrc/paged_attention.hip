@@ -7,10 +7,10 @@
 // (NT = 1, 2, 4); a verify step (k+1 positions) is a single tile, a prefill
 // is many.  Each tile only walks the keys its last row can see.  Segments
 // come from one of two decompositions:
-//   * stream (single-tile sequences of at most 16 rows, bf16 cache): per kv
-//     head the key chunks of all sequences are laid end to end and cut into
-//     one equal range per SIMD of the device, so every wave streams the same
-//     number of keys whatever the length mix;
+//   * stream (single-tile sequences of at most 16 rows, or 32 with an FP8
+//     cache): per kv head the key chunks of all sequences are laid end to
+//     end and cut into one equal range per SIMD of the device, so every wave
+//     streams the same number of keys whatever the length mix;
 //   * fixed (everything else): one wave per (kv head, sequence, query tile,
 //     768-key split), several resident per SIMD.
 // A sequence covered by one segment gets bf16 output directly; otherwise
@@ -36,8 +36,8 @@
 //     visible key so that rows past it read as zeros).  Where a SIMD holds
 //     a single wave (64-row tiles) or dequantisation lengthens the math
 //     (FP8), they are issued one chunk ahead into a second register buffer.
-// FP8 caches are dequantised to bf16 on load (exact: every e4m3 value is a
-// bf16 value).  At the end the wave transposes O^T through its LDS stage and
+// FP8 caches are dequantised to bf16 on load with the hardware conversion
+// (exact: every e4m3 value is a bf16 value).  At the end the wave transposes O^T through its LDS stage and
 // writes 16-byte rows.
 #include <stdlib.h>
 
@@ -117,18 +117,17 @@ __device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
   return static_cast<uint32_t>(f32_to_bf16(lo)) | (static_cast<uint32_t>(f32_to_bf16(hi)) << 16);
 }
 
-// 8 fp8 bytes -> 8 bf16 (exact)
+// 8 fp8 (OCP e4m3fn) bytes -> 8 bf16, exact: v_cvt_scalef32_pk_bf16_fp8 with
+// scale 1.0 converts two bytes of the selected 16-bit half (every e4m3 value,
+// subnormals included, is a bf16 value; 0x7F / 0xFF give NaN).  The kernel
+// applies k_scale / v_scale in fp32 elsewhere.
 __device__ __forceinline__ bf16x8_t fp8x8_to_bf16(uint2 w) {
-  const uint32_t in[2] = {w.x, w.y};
-  uint32_t o[4];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const uint32_t src = in[k >> 1] >> ((k & 1) * 16);
-    const uint32_t lo = __float_as_uint(e4m3_to_f32(src & 0xFFu)) >> 16;
-    const uint32_t hi = __float_as_uint(e4m3_to_f32((src >> 8) & 0xFFu)) >> 16;
-    o[k] = lo | (hi << 16);
-  }
-  uint4 r = make_uint4(o[0], o[1], o[2], o[3]);
+  const bf16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w.x, 1.0f, false);
+  const bf16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w.x, 1.0f, true);
+  const bf16x2_t c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w.y, 1.0f, false);
+  const bf16x2_t d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w.y, 1.0f, true);
+  const uint4 r = make_uint4(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b),
+                            __builtin_bit_cast(uint32_t, c), __builtin_bit_cast(uint32_t, d));
   return __builtin_bit_cast(bf16x8_t, r);
 }
 
@@ -750,8 +749,10 @@ void choose_split(int32_t num_seqs, int32_t num_kv_heads, int32_t n_qtiles, int3
 //     wave per SIMD, one chunk buffer;
 //   * up to 32 rows, bf16: fixed decomposition, one chunk buffer, three waves
 //     per SIMD hide each other's latency;
-//   * 64-row tiles and FP8: fixed decomposition with the chunk loads issued
-//     one chunk ahead (one wave per SIMD for 64 rows: no room for a second).
+//   * single-tile sequences of up to 32 rows, FP8: stream decomposition with
+//     the chunk loads issued one chunk ahead;
+//   * 64-row tiles: fixed decomposition with the loads one chunk ahead (one
+//     wave per SIMD for 64 rows: no room for a second).
 // NVA_ATTN_STREAM=0/1 and NVA_ATTN_PIPE=0/1 override the choices (tuning).
 int env_choice(const char* name) {
   const char* v = getenv(name);
@@ -760,8 +761,9 @@ int env_choice(const char* name) {
 
 bool stream_mode(int32_t num_seqs, int32_t max_q, int32_t qtile, int32_t group, bool fp8) {
   static const int forced = env_choice("NVA_ATTN_STREAM");
-  if (forced == 0 || fp8 || max_q > qtile || num_seqs > kMaxSeqGroups * kWave) return false;
-  return forced == 1 ? max_q * group <= 32 : max_q * group <= 16;
+  if (forced == 0 || max_q > qtile || num_seqs > kMaxSeqGroups * kWave) return false;
+  if (forced == 1) return max_q * group <= 32;
+  return max_q * group <= (fp8 ? 32 : 16);
 }
 
 bool pipelined(int nt, bool fp8) {
@@ -821,10 +823,17 @@ void launch_nt(const AttnParams& p, bool fp8, bool stream, dim3 grid, hipStream_
   const bool pipe = pipelined(NT, fp8);
   if constexpr (NT < 4) {
     if (stream) {
-      if (pipe)
-        paged_attention_stream_kernel<NT, false, true><<<grid, kWave, 0, s>>>(p);
-      else
-        paged_attention_stream_kernel<NT, false, false><<<grid, kWave, 0, s>>>(p);
+      if (fp8) {
+        if (pipe)
+          paged_attention_stream_kernel<NT, true, true><<<grid, kWave, 0, s>>>(p);
+        else
+          paged_attention_stream_kernel<NT, true, false><<<grid, kWave, 0, s>>>(p);
+      } else {
+        if (pipe)
+          paged_attention_stream_kernel<NT, false, true><<<grid, kWave, 0, s>>>(p);
+        else
+          paged_attention_stream_kernel<NT, false, false><<<grid, kWave, 0, s>>>(p);
+      }
       return;
     }
   }
