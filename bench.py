@@ -72,6 +72,9 @@ def parse_args():
     ap.add_argument("--roofline-repeats", type=int, default=10,
                     help="times the verify-attention launches of one step are re-issued "
                          "between HIP events for the roofline figure")
+    ap.add_argument("--reference-steps", type=int, default=3,
+                    help="steps timed with the reference's step structure for comparison "
+                         "(0 to skip)")
     ap.add_argument("--gemm-tuning", default=DEFAULT_GEMM_TUNING,
                     help="TunableOp results for the projection GEMMs ('' for library defaults)")
     ap.add_argument("--attention-only", action="store_true",
@@ -368,6 +371,30 @@ def main():
     roof = timer.measure(args.roofline_repeats, PMC_TRAFFIC_BYTES if default_workload else None)
 
     log(f"timed {args.steps} steps in {elapsed:.3f}s")
+    ref = None
+    if args.reference_steps > 0 and llm.scheduler.running:
+        # the reference's step structure on the same kernels and sequences:
+        # one warm-up step, then the timed ones
+        llm.reference_pipeline = True
+        llm.step()
+        torch.cuda.synchronize()
+        r0 = time.perf_counter()
+        ref_committed = 0
+        for _ in range(args.reference_steps):
+            _, num_tokens = llm.step()
+            ref_committed += -num_tokens
+        torch.cuda.synchronize()
+        r_el = time.perf_counter() - r0
+        llm.reference_pipeline = False
+        ref = {"value": round(ref_committed / r_el, 1), "unit": "tok/s",
+               "ms_per_step": round(r_el / args.reference_steps * 1e3, 2),
+               "steps": args.reference_steps,
+               "structure": "reference llm_engine.py:124-178 step shape on this build's kernels: "
+                            "eager draft loop with a host sync per draft step, eager target "
+                            "verify with one torch argmax + .tolist() per sequence, host "
+                            "acceptance per sequence, serial single-token draft replay per "
+                            "committed token (model_runner.py:1127-1156)"}
+        log(f"reference-structured steps: {ref['ms_per_step']} ms/step")
     cpu = None
     if cpu_batches:
         cpu = cpu_baseline(cpu_batches, args.cpu_seconds)
@@ -396,6 +423,7 @@ def main():
                    "gemm_tuning": os.path.basename(args.gemm_tuning) if args.gemm_tuning else None},
         "roofline": roof,
         "cpu_baseline": cpu,
+        "reference_pipeline": ref,
         "committed_tokens": committed,
         "accepted_drafts_per_seq_step": round(stats["accepted"] / max(stats["steps"] * n_active, 1), 4),
         "committed_per_seq_step": round(stats["committed"] / max(stats["steps"] * n_active, 1), 4),

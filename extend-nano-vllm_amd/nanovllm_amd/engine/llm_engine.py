@@ -48,6 +48,9 @@ class LLMEngine:
             config.eos = eos[0] if isinstance(eos, (list, tuple)) else (eos if eos is not None else -1)
         self.scheduler = Scheduler(config)
         self.spec_stats = {"steps": 0, "drafted": 0, "accepted": 0, "committed": 0}
+        # comparison runs: execute speculative steps with the reference's
+        # structure (see _reference_speculative_step)
+        self.reference_pipeline = False
         atexit.register(self.exit)
 
     def exit(self):
@@ -82,7 +85,8 @@ class LLMEngine:
         seqs, is_prefill = self.scheduler.schedule()
         scheduled = sum(seq.num_scheduled_tokens for seq in seqs)
         if self.config.speculative_config is not None and not is_prefill:
-            num_tokens = -self._speculative_step(seqs)
+            step = self._reference_speculative_step if self.reference_pipeline else self._speculative_step
+            num_tokens = -step(seqs)
         else:
             token_ids = self.model_runner.call("run", seqs, is_prefill)
             self.scheduler.postprocess(seqs, token_ids, is_prefill)
@@ -128,6 +132,38 @@ class LLMEngine:
         if commit_seqs:
             self.model_runner.call("commit_eagle3_batch", commit_seqs, commit_tokens,
                                    commit_starts)
+        committed = sum(len(seq) - base for seq, base in zip(seqs, bases))
+        self.spec_stats["steps"] += 1
+        self.spec_stats["committed"] += committed
+        return committed
+
+    def _reference_speculative_step(self, seqs: list[Sequence]) -> int:
+        """One EAGLE3 step in the reference's structure (llm_engine.py:124-178):
+        proposals with a host sync per draft step, per-sequence argmax and
+        host rule, and a serial single-token draft replay per committed token.
+        Same kernels as the engine's own step; used to time the reference's
+        pipeline shape on this hardware."""
+        runner = self.model_runner
+        for seq in seqs:
+            self.scheduler.reserve_speculation(seq)
+        proposals = runner.call("propose_eagle3_batch_reference", seqs)
+        bases = []
+        for seq, proposal in zip(seqs, proposals):
+            bases.append(self.scheduler.begin_speculation(seq, proposal))
+            seq.num_computed_tokens = bases[-1] - 1
+        targets, aux = runner.call("verify_eagle3_batch_reference", seqs,
+                                   [len(p) + 1 for p in proposals])
+        for seq, proposal, base, target, rows in zip(seqs, proposals, bases, targets, aux):
+            v = verify_greedy_proposals(proposal, target)
+            self.spec_stats["drafted"] += len(proposal)
+            self.spec_stats["accepted"] += v.accepted_count
+            self.scheduler.postprocess_speculation(seq, base, v.accepted_tokens,
+                                                   v.replacement_token)
+            tail = seq.token_ids[base:]
+            if tail and not seq.is_finished:
+                runner.call("commit_eagle3_serial", seq, tail, rows, base - 1)
+            if seq.is_finished:
+                runner.call("release_eagle3_state", seq.seq_id)
         committed = sum(len(seq) - base for seq, base in zip(seqs, bases))
         self.spec_stats["steps"] += 1
         self.spec_stats["committed"] += committed

@@ -417,11 +417,14 @@ class ModelRunner:
             table = self._propose_eager(seqs, state_rows, steps, pos, slots, ctx_lens, lens)
         return [[table[s][i] for s in range(limits[i])] for i in range(len(seqs))]
 
-    def _propose_eager(self, seqs, state_rows, steps, pos, slots, ctx_lens, lens):
+    def _propose_eager(self, seqs, state_rows, steps, pos, slots, ctx_lens, lens,
+                       sync_each_step: bool = False):
         try:
             hidden = self.state_hidden.index_select(0, state_rows)
             feedback = self.state_feedback.index_select(0, state_rows)
             tokens = [self.eagle3_model.sample_greedy(hidden)]
+            if sync_each_step:
+                tokens[-1].tolist()
             if steps > 1:
                 pos_d = _pinned(pos, torch.int64).to(self.device, non_blocking=True)
                 slot_d = _pinned(slots, torch.int32).to(self.device, non_blocking=True)
@@ -433,9 +436,62 @@ class ModelRunner:
                     hidden, feedback = self.eagle3_model.forward_with_cache(tokens[-1], pos_d[s],
                                                                             feedback)
                     tokens.append(self.eagle3_model.sample_greedy(hidden))
+                    if sync_each_step:
+                        tokens[-1].tolist()
             return torch.stack(tokens).cpu().tolist()
         finally:
             reset_context()
+
+    # ------------------------------------------------------------ reference-structured step
+    # The reference's step structure (model_runner.py:1047-1078, 1127-1156,
+    # 1159-1249) on this build's kernels, for comparison runs: a host sync
+    # after every draft step, one argmax and one device->host copy per
+    # sequence in verify, and one single-token draft forward per committed
+    # token.  The engine's own step does not use these.
+
+    @torch.inference_mode()
+    def propose_eagle3_batch_reference(self, seqs: list[Sequence]) -> list[list[int]]:
+        k = self.speculative_config.num_speculative_tokens
+        limits = [min(k, seq.max_tokens - seq.num_completion_tokens) for seq in seqs]
+        steps = max(limits, default=0)
+        if steps <= 0:
+            return [[] for _ in seqs]
+        lens = [len(seq) for seq in seqs]
+        pos = [[n - 1 + s for n in lens] for s in range(steps - 1)]
+        slots = [[self._slot(seq, p) for seq, p in zip(seqs, row)] for row in pos]
+        ctx_lens = [[p + 1 for p in row] for row in pos]
+        state_rows = _pinned(self._state_rows(seqs), torch.int64).to(self.device, non_blocking=True)
+        table = self._propose_eager(seqs, state_rows, steps, pos, slots, ctx_lens, lens,
+                                    sync_each_step=True)
+        return [[table[s][i] for s in range(limits[i])] for i in range(len(seqs))]
+
+    @torch.inference_mode()
+    def verify_eagle3_batch_reference(self, seqs: list[Sequence], num_input_tokens: list[int]):
+        try:
+            for seq, n in zip(seqs, num_input_tokens):
+                seq.num_scheduled_tokens = n
+            input_ids, positions = self.prepare_prefill(seqs)
+            hidden, aux = self.model.forward_with_aux_hidden_states(
+                input_ids, positions, self.speculative_config.aux_hidden_state_layers)
+            logits = self.model.compute_all_logits(hidden)
+            _, cu = self._host_prefill
+            full = aux_concat(aux)
+            targets = [logits[cu[i]:cu[i + 1]].argmax(dim=-1).tolist() for i in range(len(seqs))]
+            return targets, [full[cu[i]:cu[i + 1]] for i in range(len(seqs))]
+        finally:
+            for seq in seqs:
+                seq.num_scheduled_tokens = 0
+            reset_context()
+
+    @torch.inference_mode()
+    def commit_eagle3_serial(self, seq: Sequence, output_tokens: list[int],
+                             target_aux_hidden_states: torch.Tensor, start_position: int) -> None:
+        if not output_tokens or seq.is_finished:
+            return
+        combined = self.eagle3_model.combine_hidden_states(
+            target_aux_hidden_states[:len(output_tokens)])
+        for i, tok in enumerate(output_tokens):
+            self._draft_commit([seq], [[tok]], [start_position + i], combined[i:i + 1])
 
     def _verify_metadata(self, seqs):
         """Host lists of the verify window [num_computed, +scheduled) of every
