@@ -29,10 +29,10 @@ def dirs(tmp_path_factory):
     return target, draft
 
 
-def make_llm(dirs, spec=True, k=4, blocks=96, eager=True):
+def make_llm(dirs, spec=True, k=4, blocks=96, eager=True, kv_cache_dtype="auto"):
     target, draft = dirs
     kw = dict(load_format="dummy", seed=0, max_model_len=2048, num_kvcache_blocks=blocks,
-              enforce_eager=eager, max_num_batched_tokens=4096)
+              enforce_eager=eager, max_num_batched_tokens=4096, kv_cache_dtype=kv_cache_dtype)
     if spec:
         kw["speculative_config"] = {"method": "eagle3", "model": draft,
                                     "num_speculative_tokens": k, "aux_hidden_state_layers": AUX}
@@ -200,3 +200,49 @@ def test_hip_graph_steps_are_greedy(dirs):
             assert_same_greedy_path(graphed, p, a, b)
     finally:
         graphed.exit()
+
+
+def test_reference_structured_step_is_greedy(dirs):
+    """The reference-shaped step (host sync per draft step, per-sequence
+    argmax, serial single-token draft replay) emits the same greedy paths as
+    the engine's batched step."""
+    ps = prompts(4, seed=11)
+    sp = SamplingParams(temperature=0.0, max_tokens=21, ignore_eos=True)
+    fast = make_llm(dirs, spec=True)
+    try:
+        ref = [o["token_ids"] for o in fast.generate(ps, sp, use_tqdm=False)]
+    finally:
+        fast.exit()
+    slow = make_llm(dirs, spec=True)
+    slow.reference_pipeline = True
+    try:
+        got = [o["token_ids"] for o in slow.generate(ps, sp, use_tqdm=False)]
+        assert slow.spec_stats["steps"] > 0
+        for p, a, b in zip(ps, got, ref):
+            assert_same_greedy_path(slow, p, a, b)
+    finally:
+        slow.exit()
+
+
+def test_fp8_kv_cache_spec_equals_target_greedy(dirs):
+    """EAGLE3 over an FP8 E4M3 KV cache (which the reference does not allow):
+    the speculative engine emits the greedy path of the FP8-cache target,
+    including prompts that prefill several query tiles."""
+    ps = prompts(4, seed=12, lo=200, hi=600)
+    sp = SamplingParams(temperature=0.0, max_tokens=25, ignore_eos=True)
+    spec = make_llm(dirs, spec=True, kv_cache_dtype="fp8")
+    try:
+        assert spec.model_runner.kv_cache.dtype == torch.float8_e4m3fn
+        outs = [o["token_ids"] for o in spec.generate(ps, sp, use_tqdm=False)]
+        for p, o in zip(ps, outs):
+            assert len(o) == 25
+            assert check_greedy(spec, p, o) == []
+    finally:
+        spec.exit()
+    plain = make_llm(dirs, spec=False, kv_cache_dtype="fp8")
+    try:
+        ref = [o["token_ids"] for o in plain.generate(ps, sp, use_tqdm=False)]
+        for p, a, b in zip(ps, outs, ref):
+            assert_same_greedy_path(plain, p, a, b)
+    finally:
+        plain.exit()
