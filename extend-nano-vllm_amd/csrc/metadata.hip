@@ -1,0 +1,116 @@
+// Verify-batch metadata on the device: the per-token loops of the
+// reference's prepare_prefill (nanovllm/engine/model_runner.py:761-800)
+// derived from per-sequence (first position, query length) and the block
+// tables, so a step uploads O(sequences) values instead of O(tokens).
+//
+// One workgroup: the sequence prefix sums are a block-wide scan in LDS, then
+// every thread derives the positions and slots of a strided set of tokens
+// (sequence found by binary search over the scanned offsets).  The work is
+// a few thousand integers; the point is removing host work, not bandwidth.
+#include "common.h"
+
+namespace nva {
+namespace {
+
+constexpr int kMetaThreads = 256;
+constexpr int kMaxMetaSeqs = 2048;
+
+// inclusive block scan of one value per thread (kMetaThreads values)
+__device__ int block_scan(int v, int* sh) {
+  const int tid = threadIdx.x;
+  sh[tid] = v;
+  __syncthreads();
+  for (int d = 1; d < kMetaThreads; d <<= 1) {
+    const int u = tid >= d ? sh[tid - d] : 0;
+    __syncthreads();
+    sh[tid] += u;
+    __syncthreads();
+  }
+  const int r = sh[tid];
+  __syncthreads();
+  return r;
+}
+
+__global__ void __launch_bounds__(kMetaThreads)
+verify_metadata_kernel(const int32_t* __restrict__ start_pos, const int32_t* __restrict__ q_lens,
+                       int32_t num_seqs, const int32_t* __restrict__ block_tables,
+                       int64_t bt_stride, int32_t max_blocks, int32_t block_size,
+                       int32_t* __restrict__ cu_q_out, int32_t* __restrict__ cu_k_out,
+                       int64_t* __restrict__ positions, int32_t* __restrict__ slots,
+                       int32_t num_tokens) {
+  __shared__ int cu_q[kMaxMetaSeqs + 1];
+  __shared__ int cu_k[kMaxMetaSeqs + 1];
+  __shared__ int scan[kMetaThreads];
+  const int tid = threadIdx.x;
+  if (tid == 0) {
+    cu_q[0] = 0;
+    cu_k[0] = 0;
+  }
+  int carry_q = 0, carry_k = 0;
+  for (int base = 0; base < num_seqs; base += kMetaThreads) {
+    const int i = base + tid;
+    const int q = i < num_seqs ? q_lens[i] : 0;
+    const int k = i < num_seqs ? start_pos[i] + q : 0;
+    const int iq = block_scan(q, scan) + carry_q;
+    const int ik = block_scan(k, scan) + carry_k;
+    if (i < num_seqs) {
+      cu_q[i + 1] = iq;
+      cu_k[i + 1] = ik;
+    }
+    __syncthreads();
+    const int last = (num_seqs - base < kMetaThreads ? num_seqs - base : kMetaThreads);
+    carry_q = cu_q[base + last];
+    carry_k = cu_k[base + last];
+    __syncthreads();
+  }
+  for (int i = tid; i <= num_seqs; i += kMetaThreads) {
+    cu_q_out[i] = cu_q[i];
+    cu_k_out[i] = cu_k[i];
+  }
+  const int total = cu_q[num_seqs];
+  for (int t = tid; t < num_tokens; t += kMetaThreads) {
+    int64_t pos = 0;
+    int32_t slot = -1;
+    if (t < total) {
+      // sequence s with cu_q[s] <= t < cu_q[s + 1] (empty sequences skipped)
+      int lo = 0, hi = num_seqs;
+      while (hi - lo > 1) {
+        const int mid = (lo + hi) >> 1;
+        if (cu_q[mid] <= t) lo = mid; else hi = mid;
+      }
+      const int p = start_pos[lo] + (t - cu_q[lo]);
+      pos = p;
+      const int b = p / block_size;
+      if (p >= 0 && b < max_blocks) {
+        const int32_t id = block_tables[static_cast<int64_t>(lo) * bt_stride + b];
+        if (id >= 0) slot = id * block_size + p % block_size;
+      }
+    }
+    positions[t] = pos;
+    slots[t] = slot;
+  }
+}
+
+}  // namespace
+}  // namespace nva
+
+using namespace nva;
+
+extern "C" int nva_verify_metadata(const int32_t* start_pos, const int32_t* q_lens,
+                                   int32_t num_seqs, const int32_t* block_tables,
+                                   int64_t block_table_stride, int32_t max_blocks_per_seq,
+                                   int32_t block_size, int32_t* cu_seqlens_q,
+                                   int32_t* cu_seqlens_k, int64_t* positions,
+                                   int32_t* slot_mapping, int32_t num_tokens, void* stream) {
+  if (num_seqs < 0 || num_tokens < 0 || block_size <= 0 || max_blocks_per_seq < 0) return NVA_ERR_ARG;
+  if (num_seqs > kMaxMetaSeqs) return NVA_ERR_UNSUPPORTED;
+  if (block_table_stride < max_blocks_per_seq) return NVA_ERR_ARG;
+  if (!cu_seqlens_q || !cu_seqlens_k || (num_tokens > 0 && (!positions || !slot_mapping)))
+    return NVA_ERR_ARG;
+  if (num_seqs > 0 && (!start_pos || !q_lens || (max_blocks_per_seq > 0 && !block_tables)))
+    return NVA_ERR_ARG;
+  verify_metadata_kernel<<<1, kMetaThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      start_pos, q_lens, num_seqs, block_tables, block_table_stride, max_blocks_per_seq, block_size,
+      cu_seqlens_q, cu_seqlens_k, positions, slot_mapping, num_tokens);
+  return launch_status();
+}

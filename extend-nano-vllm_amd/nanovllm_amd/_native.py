@@ -53,6 +53,7 @@ SIGNATURES = {
     "nva_qk_norm_rope": (_INT, [_P, _I64, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _F32, _P,
                                 _P, _P]),
     "nva_silu_mul": (_INT, [_P, _I64, _P, _I64, _I32, _I32, _P]),
+    "nva_verify_metadata": (_INT, [_P, _P, _I32, _P, _I64, _I32, _I32, _P, _P, _P, _P, _I32, _P]),
 }
 
 

@@ -82,15 +82,22 @@ class _GraphBase:
 
 
 class VerifyGraph(_GraphBase):
+    """The host uploads per-sequence first positions and query lengths, the
+    block tables and the input ids; positions, slot mapping and cu_seqlens
+    are derived on the device inside the graph (nva_verify_metadata)."""
 
     def __init__(self, runner, bs: int, q: int):
         super().__init__(runner)
         self.bs, self.q, self.T = bs, q, bs * q
         T = self.T
         self.max_blocks = runner.max_blocks_per_seq
-        self.i64 = _Staging({"ids": T, "pos": T}, torch.int64, self.device)
-        self.i32 = _Staging({"cu_q": bs + 1, "cu_k": bs + 1, "slots": T,
-                             "bt": bs * self.max_blocks}, torch.int32, self.device)
+        self.i64 = _Staging({"ids": T}, torch.int64, self.device)
+        self.i32 = _Staging({"start": bs, "qlen": bs, "bt": bs * self.max_blocks}, torch.int32,
+                            self.device)
+        self.pos = torch.zeros(T, dtype=torch.int64, device=self.device)
+        self.slots = torch.zeros(T, dtype=torch.int32, device=self.device)
+        self.cu_q = torch.zeros(bs + 1, dtype=torch.int32, device=self.device)
+        self.cu_k = torch.zeros(bs + 1, dtype=torch.int32, device=self.device)
         self.out = torch.zeros(T + 2 * bs, dtype=torch.int32, device=self.device)
         self.aux = None
         # valid dummy metadata for the capture run
@@ -100,10 +107,8 @@ class VerifyGraph(_GraphBase):
     def _fill_dummy(self):
         bs, q = self.bs, self.q
         self.i64.fill("ids", [0] * self.T)
-        self.i64.fill("pos", [j for _ in range(bs) for j in range(q)])
-        self.i32.fill("cu_q", [i * q for i in range(bs + 1)])
-        self.i32.fill("cu_k", [i * q for i in range(bs + 1)])
-        self.i32.fill("slots", [-1] * self.T)
+        self.i32.fill("start", [0] * bs)
+        self.i32.fill("qlen", [q] * bs)
         self.i32.fill("bt", [-1] * (bs * self.max_blocks))
         self.i64.upload()
         self.i32.upload()
@@ -111,29 +116,29 @@ class VerifyGraph(_GraphBase):
     def _body(self):
         r = self.runner
         ids = self.i64.dev_view("ids")
-        set_context(True, self.i32.dev_view("cu_q"), self.i32.dev_view("cu_k"), self.q,
-                    r.max_seqlen_k, self.i32.dev_view("slots"), None,
-                    self.i32.dev_view("bt").view(self.bs, self.max_blocks))
+        bt = self.i32.dev_view("bt").view(self.bs, self.max_blocks)
+        K.verify_metadata(self.i32.dev_view("start"), self.i32.dev_view("qlen"), bt,
+                          r.block_size, self.T, self.cu_q, self.cu_k, self.pos, self.slots)
+        set_context(True, self.cu_q, self.cu_k, self.q, r.max_seqlen_k, self.slots, None, bt)
         try:
             hidden, aux = r.model.forward_with_aux_hidden_states(
-                ids, self.i64.dev_view("pos"), r.speculative_config.aux_hidden_state_layers)
+                ids, self.pos, r.speculative_config.aux_hidden_state_layers)
             logits = r.model.compute_all_logits(hidden)
-            K.argmax_accept(logits, self.i32.dev_view("cu_q"), ids, out=self.out)
+            K.argmax_accept(logits, self.cu_q, ids, out=self.out)
             self.aux = aux
         finally:
             reset_context()
 
-    def run(self, ids, pos, cu_q, cu_k, slots, bt_rows) -> None:
-        """Host lists for the real sequences; the rest of the bucket is padding."""
+    def run(self, ids, starts, qlens, bt_rows) -> None:
+        """Host lists for the real sequences (token ids, first position and
+        query length per sequence, block tables); the rest of the bucket is
+        padding: q rows at positions 0.. with no cache blocks."""
         bs, q, T = self.bs, self.q, self.T
         n = len(ids)
-        b = len(cu_q) - 1
+        b = len(starts)
         self.i64.fill("ids", list(ids) + [0] * (T - n))
-        self.i64.fill("pos", list(pos) + [0] * (T - n))
-        pad_cu = [cu_q[-1] + q * (i + 1) for i in range(bs - b)]
-        self.i32.fill("cu_q", list(cu_q) + pad_cu)
-        self.i32.fill("cu_k", list(cu_k) + [cu_k[-1] + q * (i + 1) for i in range(bs - b)])
-        self.i32.fill("slots", list(slots) + [-1] * (T - n))
+        self.i32.fill("start", list(starts) + [0] * (bs - b))
+        self.i32.fill("qlen", list(qlens) + [q] * (bs - b))
         flat = []
         for row in bt_rows:
             flat.extend(row + [-1] * (self.max_blocks - len(row)))

@@ -493,20 +493,6 @@ class ModelRunner:
         for i, tok in enumerate(output_tokens):
             self._draft_commit([seq], [[tok]], [start_position + i], combined[i:i + 1])
 
-    def _verify_metadata(self, seqs):
-        """Host lists of the verify window [num_computed, +scheduled) of every
-        sequence (the rows prepare_prefill builds)."""
-        ids, pos, slots, cu_q, cu_k = [], [], [], [0], [0]
-        for seq in seqs:
-            start = seq.num_computed_tokens
-            end = min(start + seq.num_scheduled_tokens, seq.num_tokens)
-            ids.extend(seq.token_ids[start:end])
-            pos.extend(range(start, end))
-            slots.extend(self._slot(seq, p) for p in range(start, end))
-            cu_q.append(cu_q[-1] + end - start)
-            cu_k.append(cu_k[-1] + end)
-        return ids, pos, slots, cu_q, cu_k
-
     @torch.inference_mode()
     def verify_eagle3_batch_fused(self, seqs: list[Sequence], num_input_tokens: list[int]):
         """Target forward over [previous token, drafts] of every sequence, then
@@ -524,11 +510,18 @@ class ModelRunner:
             if (self._use_graphs() and self.use_verify_graph and bs is not None
                     and not self.keep_verify_inputs
                     and all(n == k + 1 for n in num_input_tokens)):
-                ids, pos, slots, cu, cu_k = self._verify_metadata(seqs)
+                ids, starts, qlens, cu = [], [], [], [0]
+                for seq in seqs:
+                    start = seq.num_computed_tokens
+                    end = min(start + seq.num_scheduled_tokens, seq.num_tokens)
+                    ids.extend(seq.token_ids[start:end])
+                    starts.append(start)
+                    qlens.append(end - start)
+                    cu.append(cu[-1] + end - start)
                 graph = self._verify_graphs.get(bs)
                 if graph is None:
                     graph = self._verify_graphs[bs] = VerifyGraph(self, bs, k + 1)
-                graph.run(ids, pos, cu, cu_k, slots, [seq.block_table for seq in seqs])
+                graph.run(ids, starts, qlens, [seq.block_table for seq in seqs])
                 t_pad = graph.T
                 self._verify_host[:t_pad + 2 * bs].copy_(graph.out, non_blocking=True)
                 torch.cuda.current_stream().synchronize()

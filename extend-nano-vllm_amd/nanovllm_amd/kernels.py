@@ -476,3 +476,37 @@ def silu_mul(x: torch.Tensor) -> torch.Tensor:
     check(lib.nva_silu_mul(x.data_ptr(), x.stride(0), out.data_ptr(), out.stride(0), rows, inter,
                            _stream()), "silu_mul")
     return out
+
+
+# ---------------------------------------------------------------- verify metadata
+
+def verify_metadata(start_pos: torch.Tensor, q_lens: torch.Tensor, block_tables: torch.Tensor,
+                    block_size: int, num_tokens: int, cu_seqlens_q: torch.Tensor,
+                    cu_seqlens_k: torch.Tensor, positions: torch.Tensor,
+                    slot_mapping: torch.Tensor) -> None:
+    """Device-side prepare_prefill for verify rows (model_runner.py:761-800):
+    from per-sequence first positions and query lengths plus the block
+    tables, write cu_seqlens_q/k [B+1], positions [T] (int64) and
+    slot_mapping [T] (int32).  Rows past the last sequence get position 0
+    and slot -1."""
+    lib = _native.load()
+    _require_cuda(start_pos, q_lens, block_tables, cu_seqlens_q, cu_seqlens_k, positions,
+                  slot_mapping)
+    b = start_pos.numel()
+    for t, name in ((start_pos, "start_pos"), (q_lens, "q_lens"), (cu_seqlens_q, "cu_seqlens_q"),
+                    (cu_seqlens_k, "cu_seqlens_k"), (slot_mapping, "slot_mapping")):
+        _i32(t, name)
+    if q_lens.numel() != b or cu_seqlens_q.numel() < b + 1 or cu_seqlens_k.numel() < b + 1:
+        raise ValueError("start_pos / q_lens / cu_seqlens sizes do not match")
+    if positions.dtype != torch.int64 or positions.numel() < num_tokens or \
+            slot_mapping.numel() < num_tokens:
+        raise ValueError("positions (int64) and slot_mapping need num_tokens entries")
+    if block_tables.dtype != torch.int32 or block_tables.dim() != 2 or block_tables.stride(1) != 1 \
+            or block_tables.shape[0] < b:
+        raise TypeError("block_tables must be int32 [num_seqs, max_blocks]")
+    check(lib.nva_verify_metadata(start_pos.data_ptr(), q_lens.data_ptr(), b,
+                                  block_tables.data_ptr(), block_tables.stride(0),
+                                  block_tables.shape[1], int(block_size), cu_seqlens_q.data_ptr(),
+                                  cu_seqlens_k.data_ptr(), positions.data_ptr(),
+                                  slot_mapping.data_ptr(), int(num_tokens), _stream()),
+          "verify_metadata")

@@ -255,6 +255,27 @@ int nva_qk_norm_rope(const void *qkv, int64_t row_stride, const int64_t *positio
                      int32_t num_kv_heads, int32_t head_dim, float eps, void *q_out, void *k_out,
                      void *stream);
 
+/* ---------------------------------------------------------------------
+ * Verify-batch metadata on the device.
+ * Replaces the per-token loops of prepare_prefill for the verify rows
+ *   (nanovllm/engine/model_runner.py:761-800, block tables :755-759).
+ * Sequence i contributes q_lens[i] rows at positions start_pos[i] ..
+ *   start_pos[i] + q_lens[i] - 1 and sees start_pos[i] + q_lens[i] keys:
+ *   cu_seqlens_q[i+1] = cu_seqlens_q[i] + q_lens[i];
+ *   cu_seqlens_k[i+1] = cu_seqlens_k[i] + start_pos[i] + q_lens[i];
+ *   positions[t] = start_pos[i] + (t - cu_seqlens_q[i]);
+ *   slot_mapping[t] = block_tables[i][p / block_size] * block_size + p % block_size
+ *   for p = positions[t], or -1 when that block id is negative or past
+ *   max_blocks_per_seq (the reference pads block tables with -1).
+ * Rows t >= cu_seqlens_q[num_seqs] (up to num_tokens) get position 0 and
+ *   slot -1.  All arrays are device memory; num_seqs <= 2048.
+ * ------------------------------------------------------------------- */
+int nva_verify_metadata(const int32_t *start_pos, const int32_t *q_lens, int32_t num_seqs,
+                        const int32_t *block_tables, int64_t block_table_stride,
+                        int32_t max_blocks_per_seq, int32_t block_size, int32_t *cu_seqlens_q,
+                        int32_t *cu_seqlens_k, int64_t *positions, int32_t *slot_mapping,
+                        int32_t num_tokens, void *stream);
+
 /* SiluAndMul (nanovllm/layers/activation.py:11-14): x rows [a | b] of
  *   2*intermediate elements -> out = bf16(bf16(silu(a)) * b). */
 int nva_silu_mul(const void *x, int64_t x_row_stride, void *out, int64_t out_row_stride,

@@ -10,6 +10,8 @@ for numpy arrays.  It also holds the pure-Python restatements of the
 reference's host-side acceptance logic:
 
 * ``verify_greedy_proposals`` restates nanovllm/engine/speculative.py:11-30.
+* ``verify_metadata`` restates the per-token loops of prepare_prefill
+  (nanovllm/engine/model_runner.py:761-800) for verify rows.
 * ``reference_cpu_acceptance`` restates the per-sequence
   ``logits[start:end].argmax(dim=-1).tolist()`` loop of
   nanovllm/engine/model_runner.py:1066-1074 followed by
@@ -269,3 +271,28 @@ def reference_cpu_acceptance(logits, cu_q, input_ids):
         bonus.append(v.replacement_token)
         committed += v.accepted_count + (v.replacement_token is not None)
     return accepted, bonus, committed
+
+
+def verify_metadata(start_pos, q_lens, block_tables, block_size, num_tokens):
+    """Restates prepare_prefill's per-sequence loop for verify rows
+    (nanovllm/engine/model_runner.py:770-789): sequence i covers positions
+    start .. start + q - 1, sees start + q keys, and token position p maps to
+    slot block_table[p // block_size] * block_size + p % block_size.  Block
+    ids of -1 (the reference's padding, :755-759) give slot -1 here, and rows
+    past the last sequence get position 0 and slot -1.  Returns int numpy
+    arrays (cu_q, cu_k, positions, slots)."""
+    cu_q, cu_k, positions, slots = [0], [0], [], []
+    for i, (start, q) in enumerate(zip(start_pos, q_lens)):
+        cu_q.append(cu_q[-1] + int(q))
+        cu_k.append(cu_k[-1] + int(start) + int(q))
+        row = list(block_tables[i])
+        for p in range(int(start), int(start) + int(q)):
+            positions.append(p)
+            idx = p // block_size
+            bid = int(row[idx]) if idx < len(row) else -1
+            slots.append(bid * block_size + p % block_size if bid >= 0 else -1)
+    pad = num_tokens - len(positions)
+    positions += [0] * pad
+    slots += [-1] * pad
+    return (np.array(cu_q, np.int32), np.array(cu_k, np.int32),
+            np.array(positions[:num_tokens], np.int64), np.array(slots[:num_tokens], np.int32))

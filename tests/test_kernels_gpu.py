@@ -370,3 +370,32 @@ def test_attention_skips_invalid_block_ids(K, cuda):
             w /= w.sum()
             ref = w @ vals[256:vis, h // 4]
             assert np.abs(got[j, h] - ref).max() <= ATTN_TOL
+
+
+# ---------------------------------------------------------------- verify metadata
+
+@pytest.mark.parametrize("num_seqs,seed", [(1, 0), (64, 1), (300, 2)])
+def test_verify_metadata_matches_oracle(K, cuda, num_seqs, seed):
+    """Device prepare_prefill for verify rows: bit-exact against the
+    restatement, with empty sequences, -1 block ids, page crossings and
+    padding rows (300 sequences exercise the multi-pass scan)."""
+    g = np.random.default_rng(seed)
+    bs, width = 256, 12
+    q = g.integers(0, 8, num_seqs).astype(np.int32)
+    start = g.integers(0, bs * (width - 1) - 8, num_seqs).astype(np.int32)
+    tables = g.integers(0, 5000, (num_seqs, width)).astype(np.int32)
+    tables[g.random((num_seqs, width)) < 0.05] = -1
+    total = int(q.sum())
+    num_tokens = total + 5
+    cu_q, cu_k, pos, slots = oracle.verify_metadata(start, q, tables, bs, num_tokens)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+    o_cu_q = torch.full((num_seqs + 1,), -7, dtype=torch.int32, device=cuda)
+    o_cu_k = torch.full((num_seqs + 1,), -7, dtype=torch.int32, device=cuda)
+    o_pos = torch.full((num_tokens,), -7, dtype=torch.int64, device=cuda)
+    o_slots = torch.full((num_tokens,), -7, dtype=torch.int32, device=cuda)
+    K.verify_metadata(d(start), d(q), d(tables), bs, num_tokens, o_cu_q, o_cu_k, o_pos, o_slots)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(o_cu_q.cpu().numpy(), cu_q)
+    np.testing.assert_array_equal(o_cu_k.cpu().numpy(), cu_k)
+    np.testing.assert_array_equal(o_pos.cpu().numpy(), pos)
+    np.testing.assert_array_equal(o_slots.cpu().numpy(), slots)

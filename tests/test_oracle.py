@@ -280,3 +280,65 @@ def test_fp8_decode_restatement_within_reference_bound():
         ref = oracle.paged_attention(bits(q), kc, vc, np.array([0, 1], np.int32),
                                      np.array([n], np.int32), table, d ** -0.5)
         assert np.abs(got - ref).max() <= 2e-3
+
+
+# ---------------------------------------------------------------- verify metadata
+
+def test_verify_metadata_reference_decode_vector():
+    """tests/test_decode_context.py:26-32 of the reference: one row per
+    sequence at its last position."""
+    cu_q, cu_k, pos, slots = oracle.verify_metadata([15, 16], [1, 1], [[3], [5]], 256, 2)
+    assert pos.tolist() == [15, 16]
+    assert slots.tolist() == [3 * 256 + 15, 5 * 256 + 16]
+    assert cu_q.tolist() == [0, 1, 2] and cu_k.tolist() == [0, 16, 33]
+
+
+def test_verify_metadata_hand_worked_page_crossing():
+    # rows at positions 254..259 cross from logical block 0 (physical 7) into
+    # logical block 1 (physical 2); a padded -1 entry and padding rows follow
+    cu_q, cu_k, pos, slots = oracle.verify_metadata([254, 0], [6, 2], [[7, 2, -1], [-1, -1, -1]],
+                                                   256, 10)
+    assert pos.tolist() == [254, 255, 256, 257, 258, 259, 0, 1, 0, 0]
+    assert slots.tolist() == [7 * 256 + 254, 7 * 256 + 255, 512, 513, 514, 515, -1, -1, -1, -1]
+    assert cu_q.tolist() == [0, 6, 8] and cu_k.tolist() == [0, 260, 262]
+
+
+def test_verify_metadata_agrees_with_engine_host_path(monkeypatch):
+    """The engine's host-side prepare_prefill (the eager path, written
+    independently of the restatement) gives the same positions, slots and
+    offsets for verify windows."""
+    import random
+
+    import torch
+
+    from nanovllm_amd.context import get_context, reset_context
+    from nanovllm_amd.engine import model_runner as mr
+    from nanovllm_amd.engine.sequence import Sequence
+
+    monkeypatch.setattr(mr, "_pinned", lambda values, dtype: torch.tensor(values, dtype=dtype))
+    rng = random.Random(5)
+    runner = mr.ModelRunner.__new__(mr.ModelRunner)
+    runner.block_size = 256
+    runner.device = torch.device("cpu")
+    seqs, starts, qs, tables = [], [], [], []
+    for _ in range(7):
+        n = rng.randrange(1, 900)
+        seq = Sequence(list(range(n)))
+        seq.block_table = rng.sample(range(100), -(-n // 256))
+        q = rng.randrange(1, 7)
+        seq.num_computed_tokens = n - q
+        seq.num_scheduled_tokens = q
+        seqs.append(seq)
+        starts.append(n - q)
+        qs.append(q)
+        tables.append(seq.block_table + [-1] * (4 - len(seq.block_table)))
+    try:
+        _, pos = runner.prepare_prefill(seqs)
+        ctx = get_context()
+        ocu_q, ocu_k, opos, oslots = oracle.verify_metadata(starts, qs, tables, 256, pos.numel())
+        assert opos.tolist() == pos.tolist()
+        assert oslots.tolist() == ctx.slot_mapping.tolist()
+        assert ocu_q.tolist() == ctx.cu_seqlens_q.tolist()
+        assert ocu_k.tolist() == ctx.cu_seqlens_k.tolist()
+    finally:
+        reset_context()
