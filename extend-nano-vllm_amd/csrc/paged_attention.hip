@@ -11,8 +11,11 @@
 //     cache): per kv head the key chunks of all sequences are laid end to
 //     end and cut into one equal range per SIMD of the device, so every wave
 //     streams the same number of keys whatever the length mix;
-//   * fixed (everything else): one wave per (kv head, sequence, query tile,
-//     768-key split), several resident per SIMD.
+//   * fixed (everything else): one workgroup per (kv head, sequence, query
+//     tile, key split).  For bf16 tiles of up to 32 rows four waves share a
+//     1536-key split (wave w takes chunks w, w+4, ...) and fold their
+//     softmax states together in LDS; otherwise one wave runs a 768-key
+//     split.  Several workgroups are resident per CU.
 // A sequence covered by one segment gets bf16 output directly; otherwise
 // each segment writes a normalised fp32 partial plus its log-sum-exp and
 // combine_kernel merges them.
@@ -37,8 +40,8 @@
 //     a single wave (64-row tiles) or dequantisation lengthens the math
 //     (FP8), they are issued one chunk ahead into a second register buffer.
 // FP8 caches are dequantised to bf16 on load with the hardware conversion
-// (exact: every e4m3 value is a bf16 value).  At the end the wave transposes O^T through its LDS stage and
-// writes 16-byte rows.
+// (exact: every e4m3 value is a bf16 value).  At the end the wave transposes
+// O^T through its LDS stage and writes 16-byte rows.
 #include <stdlib.h>
 
 #include "common.h"
@@ -54,9 +57,12 @@ constexpr int kVPitch = 68;                          // dwords per staged V row
 constexpr int kVStage = kChunk * kVPitch;            // dwords of the wave's V stage
 constexpr int kAccPitch = kD + 4;                    // floats per column in the output tile
 static_assert(16 * kAccPitch + 16 <= kVStage, "output tile must fit the V stage");
-constexpr int kSplitKeys = 768;
+constexpr int kSplitKeys = 768;        // fixed decomposition, one wave per split
+constexpr int kSharedSplitKeys = 1536;  // fixed decomposition, several waves per split
 constexpr int kMinSplit = 128;
-constexpr int64_t kMinWorkgroups = 1024;
+constexpr int64_t kMinWaves = 1024;
+// a split spans at most kWave - 2 blocks; blocks hold at least kChunk tokens
+static_assert(kSharedSplitKeys / kChunk + 2 <= kWave, "default split must fit the smallest block");
 constexpr int kMaxSeqGroups = 8;        // stream mode: up to 8 * 64 sequences
 constexpr int kMinRangeChunks = 4;      // stream mode: at least 128 keys per range
 constexpr float kLog2e = 1.4426950408889634f;
@@ -152,14 +158,23 @@ __device__ __forceinline__ void seq_geometry(const AttnParams& p, int seq, int& 
 // of the `nsplit` splits covering the keys the tile can see.  A single split
 // writes the bf16 output; otherwise a normalised fp32 partial and its
 // log-sum-exp go to the workspace for combine_kernel.
-template <int NT, bool FP8, bool PIPE>
+//
+// WPS > 1 waves (one workgroup) share a segment: wave w takes chunks w,
+// w + WPS, ...; their softmax states are merged through LDS at the end and
+// wave 0 writes the result.  `vst` then holds WPS stages.
+template <int NT, bool FP8, bool PIPE, int WPS>
 __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vst, bf16x8_t* qst,
                                                const int kvh, const int seq, const int qt,
                                                const int kv_begin, const int kv_end,
                                                const int split, const int nsplit) {
-  const int lane = threadIdx.x;
+  static_assert(WPS == 1 || !PIPE, "shared segments use the single-buffer loop");
+  static_assert(WPS == 1 || NT * (8 * kWave * 16 + 2 * kWave * 4) <= 2 * kVStage * 4,
+                "a wave's merge state must fit two V stages");
+  const int lane = threadIdx.x & (kWave - 1);
+  const int wv = WPS > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x / kWave) : 0;
   const int g = lane >> 4;
   const int m16 = lane & 15;
+  uint32_t* const stage = vst + wv * kVStage;           // this wave's V stage
 
   int q_start, q_len, L;
   seq_geometry(p, seq, q_start, q_len, L);
@@ -198,10 +213,12 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
       for (int s = 0; s < 4; ++s) qv[s] = bf16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
       lim[nt] = -1;
     }
+    if (wv == 0) {
 #pragma unroll
-    for (int s = 0; s < 4; ++s) qst[(nt * 4 + s) * kWave + lane] = qv[s];
+      for (int s = 0; s < 4; ++s) qst[(nt * 4 + s) * kWave + lane] = qv[s];
+    }
   }
-  lds_wave_sync();
+  if constexpr (WPS > 1) __syncthreads(); else lds_wave_sync();
 
   float m_run[NT], l_run[NT];
   f32x4_t acc[NT][8];
@@ -295,14 +312,14 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = 8 * i + (lane >> 3);
-        uint32_t* dst = vst + row * kVPitch + (lane & 7) * 8;
+        uint32_t* dst = stage + row * kVPitch + (lane & 7) * 8;
         *reinterpret_cast<bf16x8_t*>(dst) = fp8x8_to_bf16(make_uint2(ch.v[i].x, ch.v[i].y));
         *reinterpret_cast<bf16x8_t*>(dst + 4) = fp8x8_to_bf16(make_uint2(ch.v[i].z, ch.v[i].w));
       }
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i)
-        *reinterpret_cast<uint4*>(vst + (4 * i + g) * kVPitch + m16 * 4) = ch.v[i];
+        *reinterpret_cast<uint4*>(stage + (4 * i + g) * kVPitch + m16 * 4) = ch.v[i];
     }
 
     // ---- S^T = K . Q^T: per head_dim slice s, every (key tile, query
@@ -390,7 +407,7 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int key = (j < 4) ? (4 * g + j) : (16 + 4 * g + (j - 4));
-        w[j] = vst[key * kVPitch + 16 * pp + m16];
+        w[j] = stage[key * kVPitch + 16 * pp + m16];
       }
       uint4 ev, od;
       ev.x = __builtin_amdgcn_perm(w[1], w[0], 0x05040100u);
@@ -434,12 +451,55 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
     }
     if (c == last) compute_chunk(ca);
   } else {
-    // one buffer: a second resident wave on the SIMD hides the latency
+    // one buffer: other resident waves on the SIMD hide the latency
     Chunk ca;
-    for (int c = 0; c < nchunks; ++c) {
+    for (int c = wv; c < nchunks; c += WPS) {
       load_chunk(c, ca);
       compute_chunk(ca);
     }
+  }
+
+  if constexpr (WPS > 1) {
+    // tree merge of the waves' (max, sum, accumulator) states: at each level
+    // waves [stride, 2 stride) park theirs in two stages' worth of LDS and
+    // waves [0, stride) fold them in; wave 0 finishes
+    __syncthreads();
+#pragma unroll
+    for (int stride = WPS / 2; stride >= 1; stride >>= 1) {
+      if (wv >= stride && wv < 2 * stride) {
+        float* reg = reinterpret_cast<float*>(vst + (wv - stride) * 2 * kVStage);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+#pragma unroll
+          for (int t = 0; t < 8; ++t)
+            reinterpret_cast<f32x4_t*>(reg)[(nt * 8 + t) * kWave + lane] = acc[nt][t];
+          reg[NT * 8 * kWave * 4 + (nt * 2) * kWave + lane] = m_run[nt];
+          reg[NT * 8 * kWave * 4 + (nt * 2 + 1) * kWave + lane] = l_run[nt];
+        }
+      }
+      __syncthreads();
+      if (wv < stride) {
+        const float* reg = reinterpret_cast<const float*>(vst + wv * 2 * kVStage);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          const float mb = reg[NT * 8 * kWave * 4 + (nt * 2) * kWave + lane];
+          const float lb = reg[NT * 8 * kWave * 4 + (nt * 2 + 1) * kWave + lane];
+          const float m = fmaxf(m_run[nt], mb);
+          const float fa = m_run[nt] == -INFINITY ? 0.0f : exp2f_fast(m_run[nt] - m);
+          const float fb = mb == -INFINITY ? 0.0f : exp2f_fast(mb - m);
+          m_run[nt] = m;
+          l_run[nt] = l_run[nt] * fa + lb * fb;
+#pragma unroll
+          for (int t = 0; t < 8; ++t) {
+            const f32x4_t b = reinterpret_cast<const f32x4_t*>(reg)[(nt * 8 + t) * kWave + lane];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[nt][t][i] = acc[nt][t][i] * fa + b[i] * fb;
+          }
+        }
+      }
+      __syncthreads();
+    }
+    if (wv != 0) return;
   }
 
   // ---- finish: per column sum, transpose O^T through LDS, 16-byte stores.
@@ -510,7 +570,7 @@ __device__ __forceinline__ void zero_tile(const AttnParams& p, int kvh, int seq,
   seq_geometry(p, seq, q_start, q_len, L);
   const int j0 = qt * p.qtile;
   const int jn = (q_len - j0 < p.qtile) ? q_len - j0 : p.qtile;
-  for (int idx = threadIdx.x; idx < jn * p.group * (kD / 8); idx += kWave) {
+  for (int idx = threadIdx.x; idx < jn * p.group * (kD / 8); idx += blockDim.x) {
     const int n = idx / (kD / 8), dv = idx % (kD / 8);
     const int j = j0 + n / p.group, hh = n % p.group;
     uint16_t* o = p.out + static_cast<int64_t>(q_start + j) * p.out_row_stride +
@@ -526,7 +586,7 @@ __device__ __forceinline__ void note_rows(const AttnParams& p, int seq, int qt, 
   seq_geometry(p, seq, q_start, q_len, L);
   const int j0 = qt * p.qtile;
   const int jn = (q_len - j0 < p.qtile) ? q_len - j0 : p.qtile;
-  for (int j = threadIdx.x; j < jn; j += kWave) p.row_nsplit[q_start + j0 + j] = nsplit;
+  for (int j = threadIdx.x; j < jn; j += blockDim.x) p.row_nsplit[q_start + j0 + j] = nsplit;
 }
 
 // keys the single query tile of a sequence sees, in 32-key chunks (stream mode)
@@ -543,10 +603,10 @@ __device__ __forceinline__ int stream_chunks(const AttnParams& p, int seq) {
 // splits and the empty splits that pad the grid come last.
 // Two waves per SIMD fit the register budget of tiles up to 32 columns;
 // 64-column tiles (NT = 4) need the full register file of one wave.
-template <int NT, bool FP8, bool PIPE>
-__global__ void __launch_bounds__(kWave, NT >= 4 ? 1 : 2)
+template <int NT, bool FP8, bool PIPE, int WPS>
+__global__ void __launch_bounds__(kWave * WPS, NT >= 4 ? 1 : 2)
 paged_attention_kernel(AttnParams p) {
-  __shared__ __attribute__((aligned(16))) uint32_t vst[kVStage];
+  __shared__ __attribute__((aligned(16))) uint32_t vst[kVStage * WPS];
   __shared__ bf16x8_t qst[NT * 4 * kWave];
   const int kvh = blockIdx.x;
   const int seq = blockIdx.y;
@@ -567,7 +627,7 @@ paged_attention_kernel(AttnParams p) {
   const int kv_begin = split * p.split_len;
   if (kv_begin >= kv_limit) return;
   const int kv_end = kv_begin + p.split_len < kv_limit ? kv_begin + p.split_len : kv_limit;
-  attend_segment<NT, FP8, PIPE>(p, vst, qst, kvh, seq, qt, kv_begin, kv_end, split, nsplit);
+  attend_segment<NT, FP8, PIPE, WPS>(p, vst, qst, kvh, seq, qt, kv_begin, kv_end, split, nsplit);
 }
 
 // Balanced ("stream") decomposition for one query tile per sequence (verify
@@ -652,7 +712,7 @@ paged_attention_stream_kernel(AttnParams p) {
       const int kv_end = c1 * kChunk < kv_limit ? c1 * kChunk : kv_limit;
       const int split = r - lo / rc;
       const int nsplit = (hi - 1) / rc - lo / rc + 1;
-      attend_segment<NT, FP8, PIPE>(p, vst, qst, kvh, s, 0, kv_begin, kv_end, split, nsplit);
+      attend_segment<NT, FP8, PIPE, 1>(p, vst, qst, kvh, s, 0, kv_begin, kv_end, split, nsplit);
     }
   }
 }
@@ -719,16 +779,21 @@ int32_t choose_qtile(int32_t max_q, int32_t group) {
   return max_q < qtile ? (max_q > 0 ? max_q : 1) : qtile;
 }
 
-// Split length: 768 keys (three 256-token blocks) balances work per wave
-// against the split-combine traffic on the measured configs; it shrinks (to a
-// 128-key minimum) only when fewer than kMinWorkgroups would be launched.
+// Split length: 768 keys (three 256-token blocks) for one wave per split;
+// 1536 when several waves share a split (each wave then walks every
+// waves-th chunk of it), which halves the split-combine traffic while keeping
+// each wave's share of keys near the one-wave figure.  Both were measured on
+// the Qwen3-8B verify shape (24-row tiles, 64 sequences, ~1.5k keys).  The
+// length shrinks in 128-key steps (to a 128-key minimum) only while fewer
+// than kMinWaves waves would be launched.
 void choose_split(int32_t num_seqs, int32_t num_kv_heads, int32_t n_qtiles, int32_t max_k,
-                  int32_t* split_len, int32_t* max_splits) {
+                  int32_t waves, int32_t* split_len, int32_t* max_splits) {
   const int64_t base = static_cast<int64_t>(num_seqs > 0 ? num_seqs : 1) *
-                       (num_kv_heads > 0 ? num_kv_heads : 1) * (n_qtiles > 0 ? n_qtiles : 1);
+                       (num_kv_heads > 0 ? num_kv_heads : 1) * (n_qtiles > 0 ? n_qtiles : 1) *
+                       (waves > 0 ? waves : 1);
   const int32_t mk = max_k > 1 ? max_k : 1;
-  int32_t len = kSplitKeys;
-  while (len > kMinSplit && base * ((mk + len - 1) / len) < kMinWorkgroups) len -= kMinSplit;
+  int32_t len = waves > 1 ? kSharedSplitKeys : kSplitKeys;
+  while (len > kMinSplit && base * ((mk + len - 1) / len) < kMinWaves) len -= kMinSplit;
   // NVA_ATTN_SPLIT_KEYS (a multiple of 128) fixes the split length for tuning
   static const int32_t forced = [] {
     const char* v = getenv("NVA_ATTN_SPLIT_KEYS");
@@ -747,8 +812,9 @@ void choose_split(int32_t num_seqs, int32_t num_kv_heads, int32_t n_qtiles, int3
 // (Qwen3-0.6B/8B/32B verify and draft-decode shapes):
 //   * single-tile sequences of up to 16 rows, bf16: stream decomposition, one
 //     wave per SIMD, one chunk buffer;
-//   * up to 32 rows, bf16: fixed decomposition, one chunk buffer, three waves
-//     per SIMD hide each other's latency;
+//   * up to 32 rows, bf16: fixed decomposition, one chunk buffer, four waves
+//     per workgroup sharing each split (their states merged in LDS), several
+//     workgroups per CU hiding each other's latency;
 //   * single-tile sequences of up to 32 rows, FP8: stream decomposition with
 //     the chunk loads issued one chunk ahead;
 //   * 64-row tiles: fixed decomposition with the loads one chunk ahead (one
@@ -770,6 +836,22 @@ bool pipelined(int nt, bool fp8) {
   static const int forced = env_choice("NVA_ATTN_PIPE");
   return forced >= 0 ? forced == 1 : (nt >= 4 || fp8);
 }
+
+// Waves sharing one split of the fixed decomposition.  Four for bf16 tiles
+// of up to 32 rows without the one-chunk-ahead loads (their state leaves
+// registers for four waves per SIMD); one otherwise.  NVA_ATTN_WPS=1/2/4/8
+// overrides it for those tiles (tuning).
+int segment_waves(int nt, bool fp8) {
+  if (fp8 || nt >= 4 || pipelined(nt, fp8)) return 1;
+  static const int forced = [] {
+    const char* v = getenv("NVA_ATTN_WPS");
+    const int f = v ? atoi(v) : 0;
+    return (f == 1 || f == 2 || f == 4 || f == 8) ? f : 0;
+  }();
+  return forced ? forced : 4;
+}
+
+int tile_mfmas(int32_t tile_rows) { return tile_rows <= 16 ? 1 : tile_rows <= 32 ? 2 : 4; }
 
 // Upper bound on a sequence's split count in stream mode: a range holds at
 // least kMinRangeChunks chunks, and a sequence may start mid-range.
@@ -807,8 +889,12 @@ size_t workspace_bytes(int32_t num_seqs, int32_t num_tokens, int32_t hq, int32_t
             static_cast<size_t>(num_tokens) * sizeof(int32_t) + 512;
   }
   const int32_t n_qtiles = (max_q + qtile - 1) / qtile;
-  int32_t len, ms;
-  choose_split(num_seqs, hkv, n_qtiles, max_k, &len, &ms);
+  const int nt = tile_mfmas(qtile * (hkv > 0 ? hq / hkv : 1));
+  // either KV dtype: the larger split count of the two wave choices
+  int32_t len, ms, ms_fp8;
+  choose_split(num_seqs, hkv, n_qtiles, max_k, segment_waves(nt, false), &len, &ms);
+  choose_split(num_seqs, hkv, n_qtiles, max_k, segment_waves(nt, true), &len, &ms_fp8);
+  ms = ms_fp8 > ms ? ms_fp8 : ms;
   if (ms > 1) {
     const size_t slots = static_cast<size_t>(num_tokens) * hq * ms;
     const size_t fixed = slots * kD * sizeof(float) + slots * sizeof(float) +
@@ -839,15 +925,30 @@ void launch_nt(const AttnParams& p, bool fp8, bool stream, dim3 grid, hipStream_
   }
   if (pipe) {
     if (fp8)
-      paged_attention_kernel<NT, true, true><<<grid, kWave, 0, s>>>(p);
+      paged_attention_kernel<NT, true, true, 1><<<grid, kWave, 0, s>>>(p);
     else
-      paged_attention_kernel<NT, false, true><<<grid, kWave, 0, s>>>(p);
-  } else {
-    if (fp8)
-      paged_attention_kernel<NT, true, false><<<grid, kWave, 0, s>>>(p);
-    else
-      paged_attention_kernel<NT, false, false><<<grid, kWave, 0, s>>>(p);
+      paged_attention_kernel<NT, false, true, 1><<<grid, kWave, 0, s>>>(p);
+    return;
   }
+  if constexpr (NT < 4) {
+    switch (fp8 ? 1 : segment_waves(NT, false)) {
+      case 2:
+        paged_attention_kernel<NT, false, false, 2><<<grid, 2 * kWave, 0, s>>>(p);
+        return;
+      case 4:
+        paged_attention_kernel<NT, false, false, 4><<<grid, 4 * kWave, 0, s>>>(p);
+        return;
+      case 8:
+        paged_attention_kernel<NT, false, false, 8><<<grid, 8 * kWave, 0, s>>>(p);
+        return;
+      default:
+        break;
+    }
+  }
+  if (fp8)
+    paged_attention_kernel<NT, true, false, 1><<<grid, kWave, 0, s>>>(p);
+  else
+    paged_attention_kernel<NT, false, false, 1><<<grid, kWave, 0, s>>>(p);
 }
 
 int run_attention(AttnParams& p, int kv_dtype, void* workspace, size_t workspace_bytes_, hipStream_t s) {
@@ -881,7 +982,8 @@ int run_attention(AttnParams& p, int kv_dtype, void* workspace, size_t workspace
     p.split_len = 0;
     grid = dim3(p.hkv, stream_ranges_per_head(p.hkv), 1);
   } else {
-    choose_split(p.num_seqs, p.hkv, p.n_qtiles, p.max_k, &p.split_len, &p.max_splits);
+    choose_split(p.num_seqs, p.hkv, p.n_qtiles, p.max_k, segment_waves(tile_mfmas(tile_rows), fp8),
+                 &p.split_len, &p.max_splits);
     // the kernel keeps one block id per lane: a split may touch at most kWave blocks
     if (p.split_len / p.block_size + 2 > kWave) return NVA_ERR_UNSUPPORTED;
     grid = dim3(p.hkv, p.num_seqs, p.max_splits * p.n_qtiles);
@@ -897,7 +999,7 @@ int run_attention(AttnParams& p, int kv_dtype, void* workspace, size_t workspace
     p.ws_o = nullptr;
     p.ws_lse = nullptr;
   }
-  const int nt = (tile_rows + 15) / 16;
+  const int nt = tile_mfmas(tile_rows);
   if (nt <= 1)
     launch_nt<1>(p, fp8, stream, grid, s);
   else if (nt == 2)
