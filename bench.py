@@ -77,6 +77,8 @@ def parse_args():
                          "(0 to skip)")
     ap.add_argument("--gemm-tuning", default=DEFAULT_GEMM_TUNING,
                     help="TunableOp results for the projection GEMMs ('' for library defaults)")
+    ap.add_argument("--kv-layout", default="head_major", choices=["head_major", "token_major"],
+                    help="physical order inside a KV page (the engine's kv_cache_layout)")
     ap.add_argument("--attention-only", action="store_true",
                     help="run only the verify-attention launches of the workload and a "
                          "1 GiB copy (for hardware-counter runs); prints their own JSON")
@@ -226,6 +228,9 @@ def attention_only(args) -> None:
         off += n
     kc = torch.randn(total, block, hkv, d, generator=g).to(torch.bfloat16).to(dev)
     vc = torch.randn(total, block, hkv, d, generator=g).to(torch.bfloat16).to(dev)
+    if args.kv_layout == "head_major":  # the engine's page order, same logical view
+        kc = kc.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+        vc = vc.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
     T = args.batch * q_len
     q = torch.randn(T, hq, d, generator=g).to(torch.bfloat16).to(dev)
     cu_q = torch.arange(0, T + 1, q_len, dtype=torch.int32).to(dev)
@@ -260,6 +265,7 @@ def attention_only(args) -> None:
     copy_us = timed(lambda: dst.copy_(src), args.roofline_repeats)
     byts = sum(seqlens) * hkv * d * 2 * 2 + T * hq * d * 2 * 2
     print(json.dumps({"workload": "verify attention only", "batch": args.batch, "q_len": q_len,
+                      "kv_layout": args.kv_layout,
                       "sum_seqlen_k": sum(seqlens), "longest_seq": max(seqlens),
                       "attention_calls": n_attn + 3, "attention_us": round(attn_us, 2),
                       "bytes_per_call": byts,
@@ -300,7 +306,7 @@ def main():
     llm = LLM(target, load_format="dummy", seed=0, max_num_seqs=args.batch,
               max_model_len=max_len, num_kvcache_blocks=args.batch * blocks_per_seq + 8,
               max_num_batched_tokens=16384, enable_prefill_batching=True,
-              enforce_eager=args.eager,
+              enforce_eager=args.eager, kv_cache_layout=args.kv_layout,
               gemm_tuning_file=(args.gemm_tuning or None) if args.preset == "qwen3-8b" else None,
               speculative_config={"method": "eagle3", "model": draft,
                                   "num_speculative_tokens": args.k,
@@ -419,7 +425,7 @@ def main():
                    "preset": args.preset, "batch": args.batch, "k": args.k,
                    "prompt_len": [args.prompt_min, args.prompt_max],
                    "max_tokens": args.max_tokens, "active_seqs": n_active,
-                   "hip_graphs": not args.eager,
+                   "hip_graphs": not args.eager, "kv_layout": args.kv_layout,
                    "gemm_tuning": os.path.basename(args.gemm_tuning) if args.gemm_tuning else None},
         "roofline": roof,
         "cpu_baseline": cpu,

@@ -36,6 +36,8 @@ SIGNATURES = {
     "nva_version": (ctypes.c_char_p, []),
     "nva_store_kvcache": (_INT, [_P, _I64, _P, _I64, _P, _P, _INT, _P, _I32, _I32, _I32, _I64,
                                  _P, _P, _P]),
+    "nva_store_kvcache_paged": (_INT, [_P, _I64, _P, _I64, _P, _P, _INT, _I64, _I64, _I64, _I32,
+                                       _I32, _P, _I32, _I32, _I32, _P, _P, _P]),
     "nva_rollback": (_INT, [_P, _P, _I32, _P, _P, _P, _P, _INT, _I32, _I64, _I32, _I64, _INT, _P]),
     "nva_aux_gather": (_INT, [_P, _P, _I32, _I64, _I32, _I32, _P, _I32, _P, _I64, _P]),
     "nva_argmax_workspace_size": (_SZ, [_I32, _I32, _I32]),

@@ -51,6 +51,12 @@ class Config:
     kvcache_block_size: int = 256
     num_kvcache_blocks: int = -1
     kv_cache_dtype: str = "auto"
+    # physical order inside a KV page: "head_major" stores each kv head's
+    # block_size rows contiguously ([blocks, Hkv, block_size, D]), which
+    # spreads one head's rows over all HBM channels; "token_major" is the
+    # reference's [blocks, block_size, Hkv, D].  Both are exposed to the
+    # layers as the same [blocks, block_size, Hkv, D] view.
+    kv_cache_layout: str = "head_major"
     speculative_config: SpeculativeConfig | dict | None = None
     quantization: str | None = None
     load_format: str = "auto"
@@ -68,6 +74,8 @@ class Config:
             raise ValueError("this build runs on one GPU: data/tensor/pipeline parallel sizes must be 1")
         if self.kv_cache_dtype not in ("auto", "fp8"):
             raise ValueError("kv_cache_dtype must be 'auto' or 'fp8'")
+        if self.kv_cache_layout not in ("head_major", "token_major"):
+            raise ValueError("kv_cache_layout must be 'head_major' or 'token_major'")
         if self.quantization is not None:
             raise ValueError("weight quantization is not part of this build")
         if self.load_format not in ("auto", "dummy"):

@@ -202,6 +202,19 @@ class ModelRunner:
     def _kv_dtype(self):
         return torch.float8_e4m3fn if self.config.kv_cache_dtype == "fp8" else self.dtype
 
+    def _kv_pages(self, kinds, layers, num_blocks, num_kv_heads, head_dim, dtype):
+        """KV pages with the reference's logical shape [2, layers, blocks,
+        block_size, Hkv, D] (model_runner.py:285-364 of the reference).  With
+        the head-major layout the storage is [2, layers, blocks, Hkv,
+        block_size, D] and this is a permuted view of it: every consumer
+        (store, attention) addresses pages through their strides."""
+        if self.config.kv_cache_layout == "head_major":
+            pages = torch.empty(kinds, layers, num_blocks, num_kv_heads, self.block_size, head_dim,
+                                dtype=dtype, device=self.device)
+            return pages.permute(0, 1, 2, 4, 3, 5)
+        return torch.empty(kinds, layers, num_blocks, self.block_size, num_kv_heads, head_dim,
+                           dtype=dtype, device=self.device)
+
     def allocate_kv_cache(self):
         config = self.config
         hf = config.hf_config
@@ -224,9 +237,8 @@ class ModelRunner:
         if num_blocks <= 0:
             raise RuntimeError("not enough GPU memory for the KV cache")
         config.num_kvcache_blocks = int(num_blocks)
-        self.kv_cache = torch.empty(2, layers, num_blocks, self.block_size,
-                                    hf.num_key_value_heads, head_dim, dtype=kv_dtype,
-                                    device=self.device)
+        self.kv_cache = self._kv_pages(2, layers, num_blocks, hf.num_key_value_heads, head_dim,
+                                       kv_dtype)
         attns = [m for m in self.model.modules() if isinstance(m, Attention)]
         assert len(attns) == layers
         for i, m in enumerate(attns):
@@ -238,9 +250,9 @@ class ModelRunner:
             # logical rollback govern both caches
             ec = self.eagle3_model.config
             d_attns = [m for m in self.eagle3_model.modules() if isinstance(m, Attention)]
-            self.eagle_kv_cache = torch.empty(2, len(d_attns), num_blocks, self.block_size,
-                                              ec.num_key_value_heads, ec.head_dim,
-                                              dtype=ec.torch_dtype, device=self.device)
+            self.eagle_kv_cache = self._kv_pages(2, len(d_attns), num_blocks,
+                                                 ec.num_key_value_heads, ec.head_dim,
+                                                 ec.torch_dtype)
             for i, m in enumerate(d_attns):
                 m.k_cache = self.eagle_kv_cache[0, i]
                 m.v_cache = self.eagle_kv_cache[1, i]

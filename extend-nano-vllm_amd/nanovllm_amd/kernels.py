@@ -120,8 +120,9 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
 
     Mirrors nanovllm.layers.attention.store_kvcache (attention.py:189-217):
     key/value [N, Hkv, D] with unit element stride and head stride D, caches
-    [num_blocks, block_size, Hkv, D] with token stride Hkv*D, slot -1 skipped;
-    FP8 caches store e4m3(x / scale)."""
+    [num_blocks, block_size, Hkv, D] (any block / token / head strides with a
+    contiguous head_dim, so head-major pages seen through a permuted view
+    work too), slot -1 skipped; FP8 caches store e4m3(x / scale)."""
     lib = _native.load()
     _require_cuda(key, value, k_cache, v_cache, slot_mapping)
     n, hkv, d = key.shape
@@ -131,13 +132,33 @@ def store_kvcache(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
         raise ValueError("key/value must have unit stride in the last dim")
     if not (key.stride(1) == d and value.stride(1) == d):
         raise ValueError("key/value head stride must equal head_dim")
+    kvd, bstr, tstr, hstr, nb, bs, c_hkv, c_d = _cache_args(k_cache, v_cache)
+    if (c_hkv, c_d) != (hkv, d):
+        raise ValueError("cache heads / head_dim do not match key")
+    if slot_mapping.numel() != n:
+        raise ValueError("slot_mapping must have one entry per token")
+    _i32(slot_mapping, "slot_mapping")
+    check(lib.nva_store_kvcache_paged(
+        key.data_ptr(), key.stride(0), value.data_ptr(), value.stride(0), k_cache.data_ptr(),
+        v_cache.data_ptr(), kvd, bstr, tstr, hstr, nb, bs, slot_mapping.data_ptr(), n, hkv, d,
+        _ptr(_scale(k_scale)), _ptr(_scale(v_scale)), _stream()), "store_kvcache")
+
+
+def store_kvcache_rows(key: torch.Tensor, value: torch.Tensor, k_cache: torch.Tensor,
+                       v_cache: torch.Tensor, slot_mapping: torch.Tensor,
+                       k_scale: torch.Tensor | None = None,
+                       v_scale: torch.Tensor | None = None) -> None:
+    """store_kvcache through the reference-shaped entry point
+    (``nva_store_kvcache``): caches with contiguous token rows only, as the
+    reference asserts (attention.py:198-203)."""
+    lib = _native.load()
+    _require_cuda(key, value, k_cache, v_cache, slot_mapping)
+    n, hkv, d = key.shape
     row = hkv * d
     if k_cache.stride(1) != row or v_cache.stride(1) != row or k_cache.stride(-1) != 1:
         raise ValueError("cache token stride must equal num_kv_heads * head_dim")
     if k_cache.dtype != v_cache.dtype:
         raise TypeError("k_cache and v_cache must share a dtype")
-    if slot_mapping.numel() != n:
-        raise ValueError("slot_mapping must have one entry per token")
     _i32(slot_mapping, "slot_mapping")
     num_slots = k_cache.shape[0] * k_cache.shape[1]
     check(lib.nva_store_kvcache(

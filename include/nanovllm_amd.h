@@ -72,6 +72,28 @@ int nva_store_kvcache(const void *key, int64_t key_row_stride,
                       int32_t num_kv_heads, int32_t head_dim, int64_t num_slots,
                       const float *k_scale, const float *v_scale, void *stream);
 
+/* The same slot write into a cache addressed by strides, for layouts other
+ * than contiguous token rows.  Replaces the same reference call
+ *   (nanovllm/layers/attention.py:189-217); the reference asserts the
+ *   token-major layout (:198-203), which is the case
+ *   cache_token_stride == num_kv_heads * head_dim, cache_head_stride ==
+ *   head_dim.
+ * k_cache/v_cache: [num_blocks, block_size, num_kv_heads, head_dim] in
+ *   element strides cache_block_stride, cache_token_stride,
+ *   cache_head_stride (unit stride over head_dim), e.g. the head-major pages
+ *   [num_blocks, num_kv_heads, block_size, head_dim] seen as
+ *   (Hkv*bs*D, D, bs*D).  Slot s is token s % block_size of block
+ *   s / block_size; slots outside [0, num_blocks * block_size) are skipped.
+ * Everything else as nva_store_kvcache. */
+int nva_store_kvcache_paged(const void *key, int64_t key_row_stride,
+                            const void *value, int64_t value_row_stride,
+                            void *k_cache, void *v_cache, int kv_dtype,
+                            int64_t cache_block_stride, int64_t cache_token_stride,
+                            int64_t cache_head_stride, int32_t num_blocks,
+                            int32_t block_size, const int32_t *slot_mapping,
+                            int32_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
+                            const float *k_scale, const float *v_scale, void *stream);
+
 /* ---------------------------------------------------------------------
  * K2b  Rollback of rejected draft rows.
  * Device mirror of the reference's logical rollback after greedy

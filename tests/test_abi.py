@@ -20,7 +20,7 @@ def declared_symbols():
 
 def test_header_declares_the_hot_path_entry_points():
     syms = declared_symbols()
-    for name in ("nva_store_kvcache", "nva_rollback", "nva_aux_gather", "nva_argmax_accept",
+    for name in ("nva_store_kvcache", "nva_store_kvcache_paged", "nva_rollback", "nva_aux_gather", "nva_argmax_accept",
                  "nva_argmax_rows", "nva_paged_attention_varlen", "nva_paged_attention_decode"):
         assert name in syms
 
@@ -43,6 +43,8 @@ def test_host_side_argument_errors_without_gpu():
     # bad arguments are rejected on the host before any launch
     assert lib.nva_store_kvcache(None, 0, None, 0, None, None, 7, None, 4, 1, 128, 10,
                                  None, None, None) == _native.NVA_ERR_ARG
+    assert lib.nva_store_kvcache_paged(None, 0, None, 0, None, None, 0, 0, 0, 0, 1, 0, None, 4,
+                                       1, 128, None, None, None) == _native.NVA_ERR_ARG
     assert lib.nva_aux_gather(None, None, 9, 0, 0, 0, None, 1, None, 0, None) == _native.NVA_ERR_ARG
     assert lib.nva_paged_attention_decode(None, 0, 0, None, None, 0, 0, 0, 0, 1, 256, None, None,
                                           0, 1, 1, 16, 8, 8, 64, 1.0, None, None, None, 0, 0,

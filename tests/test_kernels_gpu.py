@@ -137,8 +137,9 @@ def test_argmax_rows_with_index_map(K, cuda):
 
 # ---------------------------------------------------------------- K2
 
+@pytest.mark.parametrize("layout", ["token_major", "head_major", "rows_entry"])
 @pytest.mark.parametrize("fp8", [False, True])
-def test_store_kvcache_matches_oracle(K, cuda, fp8):
+def test_store_kvcache_matches_oracle(K, cuda, fp8, layout):
     g = torch.Generator().manual_seed(21)
     t, hq, hkv, d, nb, bs = 160, 16, 8, 128, 12, 256
     # key/value as views into a fused QKV output (row stride > row)
@@ -149,11 +150,18 @@ def test_store_kvcache_matches_oracle(K, cuda, fp8):
     slots[::7] = -1
     cdt = torch.float8_e4m3fn if fp8 else torch.bfloat16
     init = (torch.randn(nb, bs, hkv, d, generator=g)).to(cdt)
-    kc, vc = init.clone().to(cuda), init.clone().to(cuda)
+    if layout == "head_major":
+        # pages stored [nb, Hkv, bs, D], passed as a [nb, bs, Hkv, D] view
+        kc = init.permute(0, 2, 1, 3).contiguous().to(cuda).permute(0, 2, 1, 3)
+        vc = init.permute(0, 2, 1, 3).contiguous().to(cuda).permute(0, 2, 1, 3)
+    else:
+        kc, vc = init.clone().to(cuda), init.clone().to(cuda)
     ks = torch.tensor([1.0], device=cuda) if fp8 else None
     dq = qkv.to(cuda)
-    K.store_kvcache(dq[:, hq * d:(hq + hkv) * d].view(t, hkv, d),
-                    dq[:, (hq + hkv) * d:].view(t, hkv, d), kc, vc, slots.to(cuda), ks, ks)
+    store = K.store_kvcache_rows if layout == "rows_entry" else K.store_kvcache
+    store(dq[:, hq * d:(hq + hkv) * d].view(t, hkv, d),
+          dq[:, (hq + hkv) * d:].view(t, hkv, d), kc, vc, slots.to(cuda), ks, ks)
+    kc, vc = kc.contiguous(), vc.contiguous()
     rk, rv = bits(init).copy(), bits(init).copy()
     oracle.store_kv(bits(key.contiguous()), bits(value.contiguous()), rk, rv, slots.numpy())
     np.testing.assert_array_equal(bits(kc.cpu()), rk)
@@ -226,13 +234,18 @@ def test_aux_gather_matches_oracle(K, cuda):
 
 # ---------------------------------------------------------------- K1
 
-def _run_verify(K, cuda, case, fp8=False):
+def _run_verify(K, cuda, case, fp8=False, head_major=False):
     kc = case["k_cache"].clone()
     vc = case["v_cache"].clone()
     if fp8:
         kc = kc.float().to(torch.float8_e4m3fn)
         vc = vc.float().to(torch.float8_e4m3fn)
-    dkc, dvc = kc.to(cuda), vc.to(cuda)
+    if head_major:
+        # pages stored [blocks, Hkv, block_size, D], seen as [blocks, block_size, Hkv, D]
+        dkc = kc.permute(0, 2, 1, 3).contiguous().to(cuda).permute(0, 2, 1, 3)
+        dvc = vc.permute(0, 2, 1, 3).contiguous().to(cuda).permute(0, 2, 1, 3)
+    else:
+        dkc, dvc = kc.to(cuda), vc.to(cuda)
     one = torch.ones(1, device=cuda) if fp8 else None
     K.store_kvcache(case["k_new"].to(cuda), case["v_new"].to(cuda), dkc, dvc,
                     case["slot_mapping"].to(cuda), one, one)
@@ -246,7 +259,7 @@ def _run_verify(K, cuda, case, fp8=False):
     # oracle: store then attention on the CPU copy
     rk, rv = bits(kc).copy(), bits(vc).copy()
     oracle.store_kv(bits(case["k_new"]), bits(case["v_new"]), rk, rv, case["slot_mapping"].numpy())
-    np.testing.assert_array_equal(bits(dkc.cpu()), rk)
+    np.testing.assert_array_equal(bits(dkc.contiguous().cpu()), rk)
     ref = oracle.paged_attention(bits(case["q"]), rk, rv, case["cu_q"].numpy(),
                                  case["lens"].numpy(), case["block_tables"].numpy(), d ** -0.5)
     got = out.float().cpu().numpy()
@@ -272,6 +285,20 @@ def test_verify_attention_fp8(K, cuda):
     got, ref = _run_verify(K, cuda, case, fp8=True)
     err = np.abs(got - ref).max()
     assert err <= ATTN_TOL, err
+
+
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("name,kw", [
+    ("config3", dict(seed=8, batch=16, q_len=6, ctx_lo=256, ctx_hi=2304, hq=32, hkv=8)),
+    ("decode", dict(seed=9, batch=12, q_len=1, ctx_lo=1, ctx_hi=1200, hq=32, hkv=8)),
+    ("gqa8_k7", dict(seed=10, batch=3, q_len=8, ctx_lo=8, ctx_hi=900, hq=64, hkv=8)),
+])
+def test_verify_attention_head_major_pages(K, cuda, name, kw, fp8):
+    """The engine's head-major pages ([blocks, Hkv, block_size, D] storage):
+    the same store + attention through strided views."""
+    got, ref = _run_verify(K, cuda, paged_case(**kw), fp8=fp8, head_major=True)
+    err = np.abs(got - ref).max()
+    assert err <= ATTN_TOL, (name, fp8, err)
 
 
 def test_fp8_decode_reference_geometry(K, cuda):
