@@ -79,6 +79,10 @@ def parse_args():
                     help="TunableOp results for the projection GEMMs ('' for library defaults)")
     ap.add_argument("--kv-layout", default="head_major", choices=["head_major", "token_major"],
                     help="physical order inside a KV page (the engine's kv_cache_layout)")
+    ap.add_argument("--kernels", action="store_true",
+                    help="time each hot-path kernel alone on the seeded synthetic inputs of "
+                         "BASELINE configs 1, 2, 4 and 5 (and config 3's shapes); one JSON line "
+                         "per kernel and config")
     ap.add_argument("--attention-only", action="store_true",
                     help="run only the verify-attention launches of the workload and a "
                          "1 GiB copy (for hardware-counter runs); prints their own JSON")
@@ -279,14 +283,191 @@ def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def kernel_configs(args) -> None:
+    """Each hot-path kernel alone, at the BASELINE configs' shapes.
+
+    Seeds follow the configs' order (config 1: 0 ... config 5: 4).  Inputs
+    are device-resident before timing.  ``iters`` launches are captured in a
+    HIP graph, so that the host's launch latency does not pace the small
+    kernels, and each figure is one replay between two HIP events on the
+    replay stream, divided by ``iters``.
+    Algorithmic bytes per launch:
+      K1 attention: sum_i L_i*Hkv*D*esz*2 + T*Hq*D*2*2 (config 5: logical
+                    bytes; its prefix-shared pages are read once per sharer);
+      K2 store:     T*Hkv*D*(2 + esz)*2 (read bf16 rows, write cache rows);
+      K3 aux:       R*3H*2*2 read + R*3H*2 written;
+      K4 argmax:    rows*V*2 read."""
+    import torch
+
+    from nanovllm_amd import kernels
+    from nanovllm_amd.synthetic import QWEN3_PRESETS
+
+    dev = torch.device("cuda", 0)
+    V = QWEN3_PRESETS["qwen3-8b"]["vocab_size"]
+    D, BS = 128, 256
+
+    def timed(fn, iters=30):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(iters):
+                fn()
+        graph.replay()
+        torch.cuda.synchronize()
+        stream = torch.cuda.current_stream()
+        s = torch.cuda.Event(enable_timing=True)
+        e = torch.cuda.Event(enable_timing=True)
+        s.record(stream)
+        graph.replay()
+        e.record(stream)
+        torch.cuda.synchronize()
+        return s.elapsed_time(e) / iters * 1e3
+
+    def emit(kernel, config, us, byts, **extra):
+        gbs = byts / us / 1e3
+        print(json.dumps({"bench": "kernels", "kernel": kernel, "config": config,
+                          "us": round(us, 2), "bytes": int(byts), "GBs": round(gbs, 1),
+                          "frac": round(gbs / HBM_PEAK_GBS, 4), **extra}), flush=True)
+
+    def pages(seed, batch, q_len, lo, hi, hq, hkv, fp8=False, shared_frac=0.0):
+        g = torch.Generator().manual_seed(seed)
+        lens = torch.randint(lo, hi + 1, (batch,), generator=g).tolist()
+        nblk = [-(-L // BS) for L in lens]
+        n_shared = [int(shared_frac * n) for n in nblk]
+        pool = max(n_shared) if n_shared else 0
+        unique = sum(n - s for n, s in zip(nblk, n_shared))
+        total = pool + unique
+        perm = torch.randperm(total, generator=g)
+        bt = torch.full((batch, max(nblk)), -1, dtype=torch.int32)
+        off = pool
+        for i, (n, sh) in enumerate(zip(nblk, n_shared)):
+            bt[i, :sh] = perm[:sh].to(torch.int32)        # the shared prefix pages
+            bt[i, sh:n] = perm[off:off + n - sh].to(torch.int32)
+            off += n - sh
+        gd = torch.Generator(device=dev).manual_seed(seed)
+        shape = (total, BS, hkv, D)
+        if args.kv_layout == "head_major":
+            kc = torch.empty(total, hkv, BS, D, dtype=torch.bfloat16, device=dev).permute(0, 2, 1, 3)
+            vc = torch.empty(total, hkv, BS, D, dtype=torch.bfloat16, device=dev).permute(0, 2, 1, 3)
+        else:
+            kc = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+            vc = torch.empty(shape, dtype=torch.bfloat16, device=dev)
+        kc.normal_(0.0, 0.5, generator=gd)
+        vc.normal_(0.0, 0.5, generator=gd)
+        if fp8:
+            kc, vc = kc.to(torch.float8_e4m3fn), vc.to(torch.float8_e4m3fn)
+            if args.kv_layout == "head_major":
+                kc = kc.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+                vc = vc.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+        T = batch * q_len
+        q = torch.empty(T, hq, D, dtype=torch.bfloat16, device=dev).normal_(0.0, 0.5, generator=gd)
+        cu_q = torch.arange(0, T + 1, q_len, dtype=torch.int32, device=dev)
+        cu_k = torch.tensor([0] + lens, dtype=torch.int64).cumsum(0).to(torch.int32).to(dev)
+        slots = torch.tensor([int(bt[i, p // BS]) * BS + p % BS
+                              for i, L in enumerate(lens) for p in range(L - q_len, L)],
+                             dtype=torch.int32, device=dev)
+        phys = (pool + unique) * BS * hkv * D * (1 if fp8 else 2) * 2
+        return dict(lens=lens, kc=kc, vc=vc, q=q, cu_q=cu_q, cu_k=cu_k, bt=bt.to(dev),
+                    slots=slots, T=T, q_len=q_len, hq=hq, hkv=hkv, fp8=fp8, phys=phys)
+
+    def attention(name, c):
+        esz = 1 if c["fp8"] else 2
+        one = torch.ones(1, device=dev) if c["fp8"] else None
+        out = torch.empty_like(c["q"])
+        args_ = (c["q"], c["kc"], c["vc"], c["cu_q"], c["cu_k"], c["q_len"], max(c["lens"]),
+                 D ** -0.5, c["bt"])
+        us = timed(lambda: kernels.paged_attention_varlen(*args_, k_scale=one, v_scale=one,
+                                                          out=out))
+        byts = sum(c["lens"]) * c["hkv"] * D * esz * 2 + c["T"] * c["hq"] * D * 2 * 2
+        extra = {}
+        if c["phys"] < sum(c["lens"]) * c["hkv"] * D * esz * 2:
+            extra["unique_kv_bytes"] = int(c["phys"])
+        emit("K1 paged_attention_varlen", name, us, byts, batch=len(c["lens"]), q_len=c["q_len"],
+             heads=f"{c['hq']}/{c['hkv']}", kv="fp8" if c["fp8"] else "bf16",
+             sum_seqlen_k=sum(c["lens"]), kv_layout=args.kv_layout, **extra)
+
+    def store(name, c):
+        esz = 1 if c["fp8"] else 2
+        one = torch.ones(1, device=dev) if c["fp8"] else None
+        hkv, T = c["hkv"], c["T"]
+        qkv = torch.randn(T, (c["hq"] + 2 * hkv) * D, device=dev).to(torch.bfloat16)
+        key = qkv[:, c["hq"] * D:(c["hq"] + hkv) * D].view(T, hkv, D)
+        value = qkv[:, (c["hq"] + hkv) * D:].view(T, hkv, D)
+        us = timed(lambda: kernels.store_kvcache(key, value, c["kc"], c["vc"], c["slots"], one,
+                                                 one))
+        emit("K2 store_kvcache", name, us, T * hkv * D * (2 + esz) * 2, rows=T)
+
+    def rollback(name, c):
+        g = torch.Generator().manual_seed(7)
+        b = len(c["lens"])
+        acc = torch.randint(0, c["q_len"], (b,), generator=g).to(torch.int32).to(dev)
+        slots = c["slots"].clone()
+        seqlens = torch.tensor(c["lens"], dtype=torch.int32, device=dev)
+        us = timed(lambda: kernels.rollback(c["cu_q"], acc, slots, seqlens))
+        emit("K2 rollback (slots only)", name, us, b * 4 * 3 + c["T"] * 4, seqs=b)
+
+    # config 1: greedy acceptance, [8, 5, V] logits, drafts raised with p = 0.7
+    def acceptance(name, seed, batch, k):
+        g = torch.Generator().manual_seed(seed)
+        q_len = k + 1
+        logits = torch.randn(batch, q_len, V, generator=g)
+        prop = torch.randint(0, V, (batch, k), generator=g)
+        hit = torch.rand(batch, k, generator=g) < 0.7
+        for s_ in range(batch):
+            for j in range(k):
+                if hit[s_, j]:
+                    logits[s_, j, prop[s_, j]] = logits[s_, j].max() + 1.0
+        lg = logits.view(batch * q_len, V).to(torch.bfloat16).to(dev)
+        ids = torch.cat([torch.randint(0, V, (batch, 1), generator=g), prop], 1)
+        ids = ids.reshape(-1).to(dev)
+        cu = torch.arange(0, batch * q_len + 1, q_len, dtype=torch.int32, device=dev)
+        us = timed(lambda: kernels.argmax_accept(lg, cu, ids))
+        emit("K4 argmax_accept", name, us, batch * q_len * V * 2, rows=batch * q_len, vocab=V)
+
+    acceptance("config1 B8 k4", 0, 8, 4)
+    acceptance("config3 verify rows B64 k5", 2, 64, 5)
+
+    c2 = pages(1, 32, 5, 512, 4096, 16, 8)
+    store("config2 B32 q5", c2)
+    attention("config2 B32 q5 Qwen3-0.6B", c2)
+    rollback("config2 B32 q5", c2)
+    del c2
+
+    c3 = pages(2, 64, 6, 256, 2304, 32, 8)
+    store("config3 B64 q6", c3)
+    attention("config3 B64 q6 Qwen3-8B", c3)
+    H = QWEN3_PRESETS["qwen3-8b"]["hidden_size"]
+    hid = [torch.randn(c3["T"], H, device=dev).to(torch.bfloat16) for _ in range(3)]
+    res = [torch.randn(c3["T"], H, device=dev).to(torch.bfloat16) for _ in range(3)]
+    src = torch.arange(c3["T"], dtype=torch.int32, device=dev)
+    us = timed(lambda: kernels.aux_gather(hid, res, src))
+    emit("K3 aux_gather", "config3 R=384 H=4096 3 layers", us, c3["T"] * 3 * H * 2 * 3)
+    dec = pages(5, 64, 1, 256, 2304, 32, 8)
+    attention("config3 draft decode B64 q1", dec)
+    del c3, dec, hid, res
+
+    c4 = pages(3, 128, 5, 4096, 16384, 16, 8, fp8=True)
+    store("config4 B128 q5 fp8", c4)
+    attention("config4 B128 q5 fp8", c4)
+    del c4
+
+    c5 = pages(4, 128, 8, 2048, 8192, 64, 8, shared_frac=0.3)
+    attention("config5 B128 q8 Qwen3-32B (30% shared prefix pages)", c5)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: --gpus {args.gpus} is not supported by this build "
-              "(single-GPU hot path; see DESIGN.md for how it would shard)", file=sys.stderr)
+              "(the hot path runs on one GPU)", file=sys.stderr)
         sys.exit(2)
     if args.attention_only:
         attention_only(args)
+        return
+    if args.kernels:
+        kernel_configs(args)
         return
     import torch
 
