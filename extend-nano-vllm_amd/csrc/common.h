@@ -88,4 +88,12 @@ inline int launch_status() {
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Raw buffer descriptor over num_records bytes at base: loads at offsets
+// past the end return zeros (dword 3: 32-bit data format, no swizzle).
+constexpr int kRsrcWord3 = 0x00020000;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int num_records) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), num_records,
+                                           kRsrcWord3);
+}
+
 }  // namespace nva

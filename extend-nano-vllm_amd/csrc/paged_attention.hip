@@ -102,14 +102,6 @@ struct AttnParams {
 
 __device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Raw buffer descriptor over num_records bytes at base: loads at offsets
-// past the end return zeros (dword 3: 32-bit data format, no swizzle).
-constexpr int kRsrcWord3 = 0x00020000;
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int num_records) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), num_records,
-                                           kRsrcWord3);
-}
-
 // Orders a wave's own LDS writes and reads: LDS executes one wave's
 // operations in issue order, so the compiler must only keep program order
 // and wait for outstanding LDS operations.
@@ -168,8 +160,8 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
                                                const int kv_begin, const int kv_end,
                                                const int split, const int nsplit) {
   static_assert(WPS == 1 || !PIPE, "shared segments use the single-buffer loop");
-  static_assert(WPS == 1 || NT * (8 * kWave * 16 + 2 * kWave * 4) <= 2 * kVStage * 4,
-                "a wave's merge state must fit two V stages");
+  static_assert(WPS == 1 || (NT <= 2 && (8 * kWave * 4 + 2 * kWave) <= kVStage),
+                "a wave's parked state must fit one V stage per column tile");
   const int lane = threadIdx.x & (kWave - 1);
   const int wv = WPS > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x / kWave) : 0;
   const int g = lane >> 4;
@@ -460,46 +452,83 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
   }
 
   if constexpr (WPS > 1) {
-    // tree merge of the waves' (max, sum, accumulator) states: at each level
-    // waves [stride, 2 stride) park theirs in two stages' worth of LDS and
-    // waves [0, stride) fold them in; wave 0 finishes
+    // ---- shared segment: every wave parks its (max, sum, accumulator)
+    // state, half per column tile: tile 0 in its own V stage (free once its
+    // loop is done), tile 1 in a second bank of WPS stages that no loop
+    // touches, so no barrier is needed before parking.  After one barrier
+    // wave w finishes head_dim columns 32 pp .. 32 pp + 31 for pp = w,
+    // w + WPS, ..., folding the WPS states in wave order (deterministic), and
+    // writes them straight from registers: lane (g, m16) holds 8 consecutive
+    // values of query column m16.
+    constexpr int kAccWords = 8 * kWave * 4;
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) {
+      float* mine = reinterpret_cast<float*>(vst + (nt * WPS + wv) * kVStage);
+#pragma unroll
+      for (int t = 0; t < 8; ++t) reinterpret_cast<f32x4_t*>(mine)[t * kWave + lane] = acc[nt][t];
+      mine[kAccWords + lane] = m_run[nt];
+      mine[kAccWords + kWave + lane] = l_run[nt];
+    }
     __syncthreads();
 #pragma unroll
-    for (int stride = WPS / 2; stride >= 1; stride >>= 1) {
-      if (wv >= stride && wv < 2 * stride) {
-        float* reg = reinterpret_cast<float*>(vst + (wv - stride) * 2 * kVStage);
+    for (int nt = 0; nt < NT; ++nt) {
+      const float* st[WPS];
+      float fw[WPS];
+      float M = -INFINITY;
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-#pragma unroll
-          for (int t = 0; t < 8; ++t)
-            reinterpret_cast<f32x4_t*>(reg)[(nt * 8 + t) * kWave + lane] = acc[nt][t];
-          reg[NT * 8 * kWave * 4 + (nt * 2) * kWave + lane] = m_run[nt];
-          reg[NT * 8 * kWave * 4 + (nt * 2 + 1) * kWave + lane] = l_run[nt];
-        }
+      for (int w = 0; w < WPS; ++w) {
+        st[w] = reinterpret_cast<const float*>(vst + (nt * WPS + w) * kVStage);
+        fw[w] = st[w][kAccWords + lane];
+        M = fmaxf(M, fw[w]);
       }
-      __syncthreads();
-      if (wv < stride) {
-        const float* reg = reinterpret_cast<const float*>(vst + wv * 2 * kVStage);
+      float lsum = 0.0f;
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          const float mb = reg[NT * 8 * kWave * 4 + (nt * 2) * kWave + lane];
-          const float lb = reg[NT * 8 * kWave * 4 + (nt * 2 + 1) * kWave + lane];
-          const float m = fmaxf(m_run[nt], mb);
-          const float fa = m_run[nt] == -INFINITY ? 0.0f : exp2f_fast(m_run[nt] - m);
-          const float fb = mb == -INFINITY ? 0.0f : exp2f_fast(mb - m);
-          m_run[nt] = m;
-          l_run[nt] = l_run[nt] * fa + lb * fb;
+      for (int w = 0; w < WPS; ++w) {
+        fw[w] = fw[w] == -INFINITY ? 0.0f : exp2f_fast(fw[w] - M);
+        lsum += fw[w] * st[w][kAccWords + kWave + lane];
+      }
+      lsum += __shfl_xor(lsum, 16, kWave);
+      lsum += __shfl_xor(lsum, 32, kWave);
+      const float inv = lsum > 0.0f ? vscale / lsum : 0.0f;
+      const int n = nt * 16 + m16;
+      if (n < rows) {
+        const int j = j0 + n / p.group, hh = n % p.group;
+        const int tok = q_start + j;
+        const int h = kvh * p.group + hh;
+        const int64_t slot = (static_cast<int64_t>(tok) * p.hq + h) * p.max_splits + split;
 #pragma unroll
-          for (int t = 0; t < 8; ++t) {
-            const f32x4_t b = reinterpret_cast<const f32x4_t*>(reg)[(nt * 8 + t) * kWave + lane];
+        for (int pp = wv; pp < 4; pp += WPS) {
+          // tiles 2 pp (even d) and 2 pp + 1 (odd d): d = 32 pp + 8 g + 2 i + e
+          float o[8];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[nt][t][i] = acc[nt][t][i] * fa + b[i] * fb;
+          for (int e = 0; e < 2; ++e) {
+            f32x4_t sum = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int w = 0; w < WPS; ++w) {
+              const f32x4_t a = reinterpret_cast<const f32x4_t*>(st[w])[(2 * pp + e) * kWave + lane];
+#pragma unroll
+              for (int i = 0; i < 4; ++i) sum[i] += fw[w] * a[i];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[2 * i + e] = sum[i] * inv;
+          }
+          const int d0 = 32 * pp + 8 * g;
+          if (nsplit == 1) {
+            uint16_t* op = p.out + static_cast<int64_t>(tok) * p.out_row_stride +
+                           static_cast<int64_t>(h) * p.out_head_stride + d0;
+            *reinterpret_cast<uint4*>(op) = make_uint4(pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]),
+                                                       pack_bf16(o[4], o[5]), pack_bf16(o[6], o[7]));
+          } else {
+            float* wo = p.ws_o + slot * kD + d0;
+            *reinterpret_cast<float4*>(wo) = make_float4(o[0], o[1], o[2], o[3]);
+            *reinterpret_cast<float4*>(wo + 4) = make_float4(o[4], o[5], o[6], o[7]);
           }
         }
+        // log-sum-exp (log2 domain) of the column for combine_kernel
+        if (nsplit > 1 && wv == 0 && g == 0) p.ws_lse[slot] = lsum > 0.0f ? M + __log2f(lsum) : -INFINITY;
       }
-      __syncthreads();
     }
-    if (wv != 0) return;
+    return;
   }
 
   // ---- finish: per column sum, transpose O^T through LDS, 16-byte stores.
@@ -606,7 +635,8 @@ __device__ __forceinline__ int stream_chunks(const AttnParams& p, int seq) {
 template <int NT, bool FP8, bool PIPE, int WPS>
 __global__ void __launch_bounds__(kWave * WPS, NT >= 4 ? 1 : 2)
 paged_attention_kernel(AttnParams p) {
-  __shared__ __attribute__((aligned(16))) uint32_t vst[kVStage * WPS];
+  // WPS V stages; shared segments park their states in NT banks of WPS stages
+  __shared__ __attribute__((aligned(16))) uint32_t vst[kVStage * WPS * (WPS > 1 && NT > 1 ? NT : 1)];
   __shared__ bf16x8_t qst[NT * 4 * kWave];
   const int kvh = blockIdx.x;
   const int seq = blockIdx.y;

@@ -43,33 +43,68 @@ def test_argmax_accept_matches_oracle(K, cuda, batch, k, vocab, seed):
     np.testing.assert_array_equal(ref_am, logits.argmax(-1).numpy())
 
 
-def test_argmax_edge_values(K, cuda):
-    v = 70001
+@pytest.mark.parametrize("layout", ["odd_width", "aligned", "padded_rows"])
+def test_argmax_edge_values(K, cuda, layout):
+    """NaN / signed zero / inf / denormal / tie cases on both partial kernels:
+    an odd row width takes the element-wise kernel, 16-byte aligned rows the
+    register-resident vector kernel (with and without a tail of elements
+    past the last whole vector)."""
+    v = 70008 if layout == "aligned" else 70001
     g = torch.Generator().manual_seed(11)
-    x = torch.randn(8, v, generator=g).to(torch.bfloat16)
+    x = torch.randn(10, v, generator=g).to(torch.bfloat16)
     xb = x.view(torch.int16)
     x[0, 100] = 50.0
-    x[0, 60000] = 50.0                       # tie: first index wins
+    x[0, 60000] = 50.0                       # tie across chunks: first index wins
     xb[1, 5000] = 0x7FC1                     # NaN beats everything
-    xb[1, 70000] = -64                       # 0xFFC0 negative NaN, later
+    xb[1, 70000] = -64                       # 0xFFC0 negative NaN, later (tail element)
     x[2, :] = -1.0
     x[2, 777] = -0.0
     x[2, 778] = 0.0                          # -0 == +0 -> first
     x[3, :] = float("-inf")                  # all -inf -> 0
     x[4, :] = 3.0                            # all equal -> 0
-    x[5, v - 1] = 1e30                       # max at the last element (tail path)
+    x[5, 70000] = 1e30                       # max at the tail element
     x[6, 0] = float("inf")
     xb[7, 69999] = 0x7F80                    # +inf late
     x[7, 3] = 3e38
-    cu = torch.tensor([0, 3, 8], dtype=torch.int32)
-    ids = torch.zeros(8, dtype=torch.int64)
-    am, acc, bonus = K.argmax_accept(x.to(cuda), cu.to(cuda), ids.to(cuda))
+    x[8, :] = -1.0
+    xb[8, 50] = 0x0000
+    xb[8, 123] = 0x0001                      # smallest positive denormal beats +0
+    xb[9, :] = -32767                        # 0x8001: negative denormals
+    xb[9, 4000] = -32768                     # 0x8000: -0
+    xb[9, 6000] = 0x0000                     # +0 ties -0: first
+    cu = torch.tensor([0, 3, 8, 10], dtype=torch.int32)
+    ids = torch.zeros(10, dtype=torch.int64)
+    if layout == "padded_rows":
+        wide = torch.full((10, 70016), -1.0, dtype=torch.bfloat16)
+        wide[:, :v] = x
+        dx = wide.to(cuda)[:, :v]            # row stride 70016: 16-byte aligned rows
+    else:
+        dx = x.to(cuda)
+    am, acc, bonus = K.argmax_accept(dx, cu.to(cuda), ids.to(cuda))
     ref = oracle.argmax_bf16(bits(x))
     np.testing.assert_array_equal(ref, x.argmax(-1).numpy())
     np.testing.assert_array_equal(am.cpu().numpy(), ref)
     ra, rb = oracle.accept(cu.numpy(), ref, ids.numpy())
     np.testing.assert_array_equal(acc.cpu().numpy(), ra)
     np.testing.assert_array_equal(bonus.cpu().numpy(), rb)
+
+
+def test_argmax_vector_kernel_random_rows(K, cuda):
+    """Aligned rows of several widths (one chunk, many chunks, a short tail):
+    the vector kernel against the oracle and torch on the same bytes."""
+    g = torch.Generator().manual_seed(12)
+    for v in (8, 2048, 4104, 32768, 151936, 151943):
+        rows = 37
+        x = torch.randn(rows, v, generator=g).to(torch.bfloat16)
+        # repeated maxima inside one vector and across threads
+        x[0, : min(v, 16)] = 9.0
+        x[1, v // 2:] = 9.0
+        wide = torch.zeros(rows, (v + 7) // 8 * 8, dtype=torch.bfloat16)
+        wide[:, :v] = x
+        out = K.argmax_rows(wide.to(cuda)[:, :v])
+        ref = oracle.argmax_bf16(bits(x)).astype(np.int64)
+        np.testing.assert_array_equal(ref, x.argmax(-1).numpy())
+        np.testing.assert_array_equal(out.cpu().numpy(), ref, err_msg=f"vocab {v}")
 
 
 def test_argmax_accept_ragged_and_empty(K, cuda):
