@@ -40,8 +40,11 @@
 //     a single wave (64-row tiles) or dequantisation lengthens the math
 //     (FP8), they are issued one chunk ahead into a second register buffer.
 // FP8 caches are dequantised to bf16 on load with the hardware conversion
-// (exact: every e4m3 value is a bf16 value).  At the end the wave transposes
-// O^T through its LDS stage and writes 16-byte rows.
+// (exact: every e4m3 value is a bf16 value).  At the end each lane writes,
+// straight from its accumulators, 8 consecutive head_dim values of one query
+// column per 32-column group (16-byte bf16 stores; fp32 partials when the
+// keys are split); waves sharing a segment first park their states in LDS
+// and each finishes a quarter of head_dim.
 #include <stdlib.h>
 
 #include "common.h"
@@ -55,8 +58,6 @@ constexpr int kCombineThreads = kCombineWaves * kWave;
 constexpr int kChunk = 32;
 constexpr int kVPitch = 68;                          // dwords per staged V row
 constexpr int kVStage = kChunk * kVPitch;            // dwords of the wave's V stage
-constexpr int kAccPitch = kD + 4;                    // floats per column in the output tile
-static_assert(16 * kAccPitch + 16 <= kVStage, "output tile must fit the V stage");
 constexpr int kSplitKeys = 768;        // fixed decomposition, one wave per split
 constexpr int kSharedSplitKeys = 1536;  // fixed decomposition, several waves per split
 constexpr int kMinSplit = 128;
@@ -531,65 +532,43 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
     return;
   }
 
-  // ---- finish: per column sum, transpose O^T through LDS, 16-byte stores.
-  float* tile = reinterpret_cast<float*>(vst);               // [16 cols][kAccPitch]
-  float* col_l = tile + 16 * kAccPitch;                      // [16]
-  const int ccol = lane >> 2;                                // column handled on output
-  const int dq = lane & 3;                                   // 32 consecutive d
+  // ---- finish (one wave): per column sum, then straight from registers:
+  // lane (g, m16) holds d = 32 pp + 8 g + 0..7 of query column m16 in the
+  // tiles 2 pp (even d) and 2 pp + 1 (odd d)
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
-    float l = l_run[nt];
-    l += __shfl_xor(l, 16, kWave);
-    l += __shfl_xor(l, 32, kWave);
-#pragma unroll
-    for (int pp = 0; pp < 4; ++pp) {
-#pragma unroll
-      for (int e = 0; e < 2; ++e) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) tile[m16 * kAccPitch + 32 * pp + 2 * (4 * g + i) + e] = acc[nt][2 * pp + e][i];
-      }
-    }
-    if (g == 0) col_l[m16] = l;
-    lds_wave_sync();
-    const int n = nt * 16 + ccol;
+    float lsum = l_run[nt];
+    lsum += __shfl_xor(lsum, 16, kWave);
+    lsum += __shfl_xor(lsum, 32, kWave);
+    const float inv = lsum > 0.0f ? vscale / lsum : 0.0f;
+    const int n = nt * 16 + m16;
     if (n < rows) {
-      const float lt = col_l[ccol];
-      const float inv = lt > 0.0f ? vscale / lt : 0.0f;
-      const float* src = tile + ccol * kAccPitch + dq * 32;
       const int j = j0 + n / p.group, hh = n % p.group;
-      const int t = q_start + j;
+      const int tok = q_start + j;
       const int h = kvh * p.group + hh;
-      if (nsplit == 1) {
-        uint16_t* op = p.out + static_cast<int64_t>(t) * p.out_row_stride +
-                       static_cast<int64_t>(h) * p.out_head_stride + dq * 32;
+      const int64_t slot = (static_cast<int64_t>(tok) * p.hq + h) * p.max_splits + split;
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const float* a = src + 8 * v;
-          *reinterpret_cast<uint4*>(op + 8 * v) =
-              make_uint4(pack_bf16(a[0] * inv, a[1] * inv), pack_bf16(a[2] * inv, a[3] * inv),
-                         pack_bf16(a[4] * inv, a[5] * inv), pack_bf16(a[6] * inv, a[7] * inv));
+      for (int pp = 0; pp < 4; ++pp) {
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[2 * i + e] = acc[nt][2 * pp + e][i] * inv;
+        const int d0 = 32 * pp + 8 * g;
+        if (nsplit == 1) {
+          uint16_t* op = p.out + static_cast<int64_t>(tok) * p.out_row_stride +
+                         static_cast<int64_t>(h) * p.out_head_stride + d0;
+          *reinterpret_cast<uint4*>(op) = make_uint4(pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]),
+                                                     pack_bf16(o[4], o[5]), pack_bf16(o[6], o[7]));
+        } else {
+          float* wo = p.ws_o + slot * kD + d0;
+          *reinterpret_cast<float4*>(wo) = make_float4(o[0], o[1], o[2], o[3]);
+          *reinterpret_cast<float4*>(wo + 4) = make_float4(o[4], o[5], o[6], o[7]);
         }
-      } else {
-        const int64_t slot = (static_cast<int64_t>(t) * p.hq + h) * p.max_splits + split;
-        float* wo = p.ws_o + slot * kD + dq * 32;
-#pragma unroll
-        for (int v = 0; v < 8; ++v)
-          *reinterpret_cast<float4*>(wo + 4 * v) =
-              make_float4(src[4 * v] * inv, src[4 * v + 1] * inv, src[4 * v + 2] * inv, src[4 * v + 3] * inv);
       }
+      // log-sum-exp (log2 domain) of the column for combine_kernel
+      if (nsplit > 1 && g == 0) p.ws_lse[slot] = lsum > 0.0f ? m_run[nt] + __log2f(lsum) : -INFINITY;
     }
-    // log-sum-exp (log2 domain) of each column: lanes with g == 0 hold the
-    // column's running max and sum
-    if (nsplit > 1 && g == 0) {
-      const int n2 = nt * 16 + m16;
-      if (n2 < rows) {
-        const int j = j0 + n2 / p.group, hh = n2 % p.group;
-        const int64_t slot = (static_cast<int64_t>(q_start + j) * p.hq + kvh * p.group + hh) *
-                                 p.max_splits + split;
-        p.ws_lse[slot] = l > 0.0f ? m_run[nt] + __log2f(l) : -INFINITY;
-      }
-    }
-    lds_wave_sync();
   }
 }
 
