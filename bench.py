@@ -83,6 +83,9 @@ def parse_args():
                     help="time each hot-path kernel alone on the seeded synthetic inputs of "
                          "BASELINE configs 1, 2, 4 and 5 (and config 3's shapes); one JSON line "
                          "per kernel and config")
+    ap.add_argument("--batch-order", default="longest_first", choices=["longest_first", "drawn"],
+                    help="--kernels: sequences longest first (the engine's verify order) or "
+                         "in the order drawn")
     ap.add_argument("--attention-only", action="store_true",
                     help="run only the verify-attention launches of the workload and a "
                          "1 GiB copy (for hardware-counter runs); prints their own JSON")
@@ -217,6 +220,7 @@ def attention_only(args) -> None:
                           cfg["num_hidden_layers"])
     g = torch.Generator().manual_seed(args.seed)
     lens = torch.randint(args.prompt_min, args.prompt_max + 1, (args.batch,), generator=g).tolist()
+    lens = sorted(lens, reverse=True)  # the engine verifies its batch longest sequence first
     done = args.warmup + args.steps + 2  # tokens each sequence holds when the roofline step runs
     q_len = args.k + 1
     seqlens = [L + done + q_len for L in lens]
@@ -334,6 +338,8 @@ def kernel_configs(args) -> None:
     def pages(seed, batch, q_len, lo, hi, hq, hkv, fp8=False, shared_frac=0.0):
         g = torch.Generator().manual_seed(seed)
         lens = torch.randint(lo, hi + 1, (batch,), generator=g).tolist()
+        if args.batch_order == "longest_first":  # the engine's verify order
+            lens = sorted(lens, reverse=True)
         nblk = [-(-L // BS) for L in lens]
         n_shared = [int(shared_frac * n) for n in nblk]
         pool = max(n_shared) if n_shared else 0
@@ -386,7 +392,8 @@ def kernel_configs(args) -> None:
             extra["unique_kv_bytes"] = int(c["phys"])
         emit("K1 paged_attention_varlen", name, us, byts, batch=len(c["lens"]), q_len=c["q_len"],
              heads=f"{c['hq']}/{c['hkv']}", kv="fp8" if c["fp8"] else "bf16",
-             sum_seqlen_k=sum(c["lens"]), kv_layout=args.kv_layout, **extra)
+             sum_seqlen_k=sum(c["lens"]), kv_layout=args.kv_layout,
+             batch_order=args.batch_order, **extra)
 
     def store(name, c):
         esz = 1 if c["fp8"] else 2

@@ -509,10 +509,25 @@ class ModelRunner:
     def verify_eagle3_batch_fused(self, seqs: list[Sequence], num_input_tokens: list[int]):
         """Target forward over [previous token, drafts] of every sequence, then
         the fused argmax + accept kernel.  Returns host lists
-        (target_tokens per sequence, accept_len, bonus); the aux hidden-state
-        pairs stay on the device for ``commit_eagle3_batch``."""
+        (target_tokens per sequence, accept_len, bonus) in the caller's
+        order; the aux hidden-state pairs stay on the device for
+        ``commit_eagle3_batch``.
+
+        The forward runs the batch longest sequence first: the verify
+        attention hands its workgroups out in batch order, and longest-first
+        lets every CU pair a long key range with a shorter one (measured on
+        the Qwen3-8B verify shape: 69.6 -> 61.3 us per attention call)."""
         if len(seqs) != len(num_input_tokens):
             raise ValueError("EAGLE3 verification metadata does not match requests")
+        order = sorted(range(len(seqs)), key=lambda i: -len(seqs[i]))
+        targets, acc, bonus = self._verify_fused([seqs[i] for i in order],
+                                                 [num_input_tokens[i] for i in order])
+        out_t, out_a, out_b = [None] * len(seqs), [0] * len(seqs), [0] * len(seqs)
+        for pos, i in enumerate(order):
+            out_t[i], out_a[i], out_b[i] = targets[pos], acc[pos], bonus[pos]
+        return out_t, out_a, out_b
+
+    def _verify_fused(self, seqs: list[Sequence], num_input_tokens: list[int]):
         k = self.speculative_config.num_speculative_tokens
         b = len(seqs)
         bs = bucket_for(b)
@@ -576,9 +591,10 @@ class ModelRunner:
         """Reference-shaped result (model_runner.py:1047-1078): per-sequence
         target argmax lists and aux hidden-state rows [q_i, 3H]."""
         targets, _, _ = self.verify_eagle3_batch_fused(seqs, num_input_tokens)
-        aux, cu, _ = self._pending_verify
+        aux, cu, index = self._pending_verify
         full = aux_concat(aux)
-        return targets, [full[cu[i]:cu[i + 1]] for i in range(len(seqs))]
+        rows = [index[seq.seq_id] for seq in seqs]
+        return targets, [full[cu[i]:cu[i + 1]] for i in rows]
 
     @torch.inference_mode()
     def commit_eagle3_batch(self, seqs: list[Sequence], output_tokens: list[list[int]],
