@@ -203,11 +203,13 @@ def cpu_baseline(batches, seconds):
 def attention_only(args) -> None:
     """Verify attention alone on the bench workload's shapes, for counter runs.
 
-    The sequences are the bench's (same seeded prompt lengths) at the point
-    the roofline step verifies them: prompt + committed tokens + k+1 verify
-    rows, with random bf16 K/V in a cache whose block ids are shuffled.
-    Launches ``--roofline-repeats`` x 36 verify-attention calls (one step's
-    worth per repeat), then a plain device copy of 1 GiB as often, for
+    The sequences are the bench's (same seeded prompt lengths, longest
+    first as the engine orders them) at the point the roofline step verifies
+    them: prompt + committed tokens + k+1 verify rows, with random bf16 K/V
+    in one cache per layer (block ids shuffled), so that consecutive calls
+    read different pages as the step's layers do.  Launches
+    ``--roofline-repeats`` x 36 verify-attention calls (one step's worth per
+    repeat, layer by layer), then a plain device copy of 1 GiB as often, for
     scaling FETCH_SIZE / WRITE_SIZE counter readings to bytes."""
     import torch
 
@@ -234,11 +236,13 @@ def attention_only(args) -> None:
     for i, n in enumerate(nblk):
         bt[i, :n] = perm[off:off + n].to(torch.int32)
         off += n
-    kc = torch.randn(total, block, hkv, d, generator=g).to(torch.bfloat16).to(dev)
-    vc = torch.randn(total, block, hkv, d, generator=g).to(torch.bfloat16).to(dev)
+    gd = torch.Generator(device=dev).manual_seed(args.seed)
     if args.kv_layout == "head_major":  # the engine's page order, same logical view
-        kc = kc.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
-        vc = vc.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+        pages = torch.empty(2, layers, total, hkv, block, d, dtype=torch.bfloat16, device=dev)
+        pages = pages.permute(0, 1, 2, 4, 3, 5)
+    else:
+        pages = torch.empty(2, layers, total, block, hkv, d, dtype=torch.bfloat16, device=dev)
+    pages.normal_(generator=gd)
     T = args.batch * q_len
     q = torch.randn(T, hq, d, generator=g).to(torch.bfloat16).to(dev)
     cu_q = torch.arange(0, T + 1, q_len, dtype=torch.int32).to(dev)
@@ -248,8 +252,13 @@ def attention_only(args) -> None:
     max_k = args.prompt_max + args.max_tokens + q_len  # the engine's max_seqlen_k
     scale = d ** -0.5
 
+    layer = [0]
+
     def attn():
-        kernels.paged_attention_varlen(q, kc, vc, cu_q, cu_k, q_len, max_k, scale, bt, out=out)
+        l = layer[0]
+        layer[0] = (l + 1) % layers
+        kernels.paged_attention_varlen(q, pages[0, l], pages[1, l], cu_q, cu_k, q_len, max_k, scale,
+                                       bt, out=out)
 
     src = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
     dst = torch.empty_like(src)
@@ -335,7 +344,7 @@ def kernel_configs(args) -> None:
                           "us": round(us, 2), "bytes": int(byts), "GBs": round(gbs, 1),
                           "frac": round(gbs / HBM_PEAK_GBS, 4), **extra}), flush=True)
 
-    def pages(seed, batch, q_len, lo, hi, hq, hkv, fp8=False, shared_frac=0.0):
+    def pages(seed, batch, q_len, lo, hi, hq, hkv, fp8=False, shared_frac=0.0, copies=1):
         g = torch.Generator().manual_seed(seed)
         lens = torch.randint(lo, hi + 1, (batch,), generator=g).tolist()
         if args.batch_order == "longest_first":  # the engine's verify order
@@ -353,20 +362,22 @@ def kernel_configs(args) -> None:
             bt[i, sh:n] = perm[off:off + n - sh].to(torch.int32)
             off += n - sh
         gd = torch.Generator(device=dev).manual_seed(seed)
-        shape = (total, BS, hkv, D)
+        dt = torch.float8_e4m3fn if fp8 else torch.bfloat16
+        # `copies` caches of the same content layout, used in turn, so that
+        # caches smaller than the 256 MB last-level cache are not re-read from it
         if args.kv_layout == "head_major":
-            kc = torch.empty(total, hkv, BS, D, dtype=torch.bfloat16, device=dev).permute(0, 2, 1, 3)
-            vc = torch.empty(total, hkv, BS, D, dtype=torch.bfloat16, device=dev).permute(0, 2, 1, 3)
+            kv = torch.empty(copies, 2, total, hkv, BS, D, dtype=dt, device=dev)
+            kv = kv.permute(0, 1, 2, 4, 3, 5)
         else:
-            kc = torch.empty(shape, dtype=torch.bfloat16, device=dev)
-            vc = torch.empty(shape, dtype=torch.bfloat16, device=dev)
-        kc.normal_(0.0, 0.5, generator=gd)
-        vc.normal_(0.0, 0.5, generator=gd)
+            kv = torch.empty(copies, 2, total, BS, hkv, D, dtype=dt, device=dev)
         if fp8:
-            kc, vc = kc.to(torch.float8_e4m3fn), vc.to(torch.float8_e4m3fn)
-            if args.kv_layout == "head_major":
-                kc = kc.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
-                vc = vc.permute(0, 2, 1, 3).contiguous().permute(0, 2, 1, 3)
+            for cp in range(copies):
+                for kind in range(2):
+                    kv[cp, kind].copy_(torch.empty(total, BS, hkv, D, device=dev)
+                                       .normal_(0.0, 0.5, generator=gd))
+        else:
+            kv.normal_(0.0, 0.5, generator=gd)
+        kc, vc = kv[0, 0], kv[0, 1]
         T = batch * q_len
         q = torch.empty(T, hq, D, dtype=torch.bfloat16, device=dev).normal_(0.0, 0.5, generator=gd)
         cu_q = torch.arange(0, T + 1, q_len, dtype=torch.int32, device=dev)
@@ -375,17 +386,23 @@ def kernel_configs(args) -> None:
                               for i, L in enumerate(lens) for p in range(L - q_len, L)],
                              dtype=torch.int32, device=dev)
         phys = (pool + unique) * BS * hkv * D * (1 if fp8 else 2) * 2
-        return dict(lens=lens, kc=kc, vc=vc, q=q, cu_q=cu_q, cu_k=cu_k, bt=bt.to(dev),
+        return dict(lens=lens, kc=kc, vc=vc, kv=kv, q=q, cu_q=cu_q, cu_k=cu_k, bt=bt.to(dev),
                     slots=slots, T=T, q_len=q_len, hq=hq, hkv=hkv, fp8=fp8, phys=phys)
 
     def attention(name, c):
         esz = 1 if c["fp8"] else 2
         one = torch.ones(1, device=dev) if c["fp8"] else None
         out = torch.empty_like(c["q"])
-        args_ = (c["q"], c["kc"], c["vc"], c["cu_q"], c["cu_k"], c["q_len"], max(c["lens"]),
-                 D ** -0.5, c["bt"])
-        us = timed(lambda: kernels.paged_attention_varlen(*args_, k_scale=one, v_scale=one,
-                                                          out=out))
+        turn = [0]
+
+        def call():
+            cp = turn[0] % c["kv"].shape[0]
+            turn[0] += 1
+            kernels.paged_attention_varlen(c["q"], c["kv"][cp, 0], c["kv"][cp, 1], c["cu_q"],
+                                           c["cu_k"], c["q_len"], max(c["lens"]), D ** -0.5,
+                                           c["bt"], k_scale=one, v_scale=one, out=out)
+
+        us = timed(call)
         byts = sum(c["lens"]) * c["hkv"] * D * esz * 2 + c["T"] * c["hq"] * D * 2 * 2
         extra = {}
         if c["phys"] < sum(c["lens"]) * c["hkv"] * D * esz * 2:
@@ -436,13 +453,13 @@ def kernel_configs(args) -> None:
     acceptance("config1 B8 k4", 0, 8, 4)
     acceptance("config3 verify rows B64 k5", 2, 64, 5)
 
-    c2 = pages(1, 32, 5, 512, 4096, 16, 8)
+    c2 = pages(1, 32, 5, 512, 4096, 16, 8, copies=4)
     store("config2 B32 q5", c2)
     attention("config2 B32 q5 Qwen3-0.6B", c2)
     rollback("config2 B32 q5", c2)
     del c2
 
-    c3 = pages(2, 64, 6, 256, 2304, 32, 8)
+    c3 = pages(2, 64, 6, 256, 2304, 32, 8, copies=4)
     store("config3 B64 q6", c3)
     attention("config3 B64 q6 Qwen3-8B", c3)
     H = QWEN3_PRESETS["qwen3-8b"]["hidden_size"]
@@ -451,7 +468,7 @@ def kernel_configs(args) -> None:
     src = torch.arange(c3["T"], dtype=torch.int32, device=dev)
     us = timed(lambda: kernels.aux_gather(hid, res, src))
     emit("K3 aux_gather", "config3 R=384 H=4096 3 layers", us, c3["T"] * 3 * H * 2 * 3)
-    dec = pages(5, 64, 1, 256, 2304, 32, 8)
+    dec = pages(5, 64, 1, 256, 2304, 32, 8, copies=4)
     attention("config3 draft decode B64 q1", dec)
     del c3, dec, hid, res
 
