@@ -44,10 +44,10 @@ DEFAULT_GEMM_TUNING = os.path.join(ROOT, "extend-nano-vllm_amd", "nanovllm_amd",
 # (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch, averaged over 363 calls),
 # scaled by what the same counters read for a 1 GiB device copy in the same
 # runs: FETCH_SIZE 524300 KiB (x2.0 to bytes read), WRITE_SIZE 1048576 KiB
-# (x1.0).  attention: FETCH 159236.9, WRITE 5850.4; combine: FETCH 1875.2,
+# (x1.0).  attention: FETCH 159189.6, WRITE 5844.1; combine: FETCH 1875.2,
 # WRITE 912.0.  Only quoted for the default workload, whose shapes it was
 # measured on.
-PMC_TRAFFIC_BYTES = int(((159236.9 + 1875.2) * 2.0 + (5850.4 + 912.0) * 1.0) * 1024)
+PMC_TRAFFIC_BYTES = int(((159189.6 + 1875.2) * 2.0 + (5844.1 + 912.0) * 1.0) * 1024)
 PMC_WORKLOAD = dict(preset="qwen3-8b", batch=64, k=5, prompt_min=256, prompt_max=2048,
                     max_tokens=256, seed=2)
 METRIC = "accepted tok/s, Qwen3-8B EAGLE3 k=5 bs64; verify-attn HBM GB/s % of peak"
