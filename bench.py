@@ -238,8 +238,8 @@ def attention_only(args) -> None:
         off += n
     gd = torch.Generator(device=dev).manual_seed(args.seed)
     if args.kv_layout == "head_major":  # the engine's page order, same logical view
-        pages = torch.empty(2, layers, total, hkv, block, d, dtype=torch.bfloat16, device=dev)
-        pages = pages.permute(0, 1, 2, 4, 3, 5)
+        pages = torch.empty(layers, total, hkv, 2, block, d, dtype=torch.bfloat16, device=dev)
+        pages = pages.permute(3, 0, 1, 4, 2, 5)
     else:
         pages = torch.empty(2, layers, total, block, hkv, d, dtype=torch.bfloat16, device=dev)
     pages.normal_(generator=gd)
@@ -366,8 +366,8 @@ def kernel_configs(args) -> None:
         # `copies` caches of the same content layout, used in turn, so that
         # caches smaller than the 256 MB last-level cache are not re-read from it
         if args.kv_layout == "head_major":
-            kv = torch.empty(copies, 2, total, hkv, BS, D, dtype=dt, device=dev)
-            kv = kv.permute(0, 1, 2, 4, 3, 5)
+            kv = torch.empty(copies, total, hkv, 2, BS, D, dtype=dt, device=dev)
+            kv = kv.permute(0, 3, 1, 4, 2, 5)
         else:
             kv = torch.empty(copies, 2, total, BS, hkv, D, dtype=dt, device=dev)
         if fp8:

@@ -52,10 +52,11 @@ class Config:
     num_kvcache_blocks: int = -1
     kv_cache_dtype: str = "auto"
     # physical order inside a KV page: "head_major" stores each kv head's
-    # block_size rows contiguously ([blocks, Hkv, block_size, D]), which
-    # spreads one head's rows over all HBM channels; "token_major" is the
-    # reference's [blocks, block_size, Hkv, D].  Both are exposed to the
-    # layers as the same [blocks, block_size, Hkv, D] view.
+    # block_size K rows, then its V rows, contiguously ([layers, blocks, Hkv,
+    # 2, block_size, D]), which spreads one head's rows over all HBM
+    # channels; "token_major" is the reference's [2, layers, blocks,
+    # block_size, Hkv, D].  Both are exposed to the layers as the same
+    # [blocks, block_size, Hkv, D] K and V views.
     kv_cache_layout: str = "head_major"
     speculative_config: SpeculativeConfig | dict | None = None
     quantization: str | None = None

@@ -205,13 +205,15 @@ class ModelRunner:
     def _kv_pages(self, kinds, layers, num_blocks, num_kv_heads, head_dim, dtype):
         """KV pages with the reference's logical shape [2, layers, blocks,
         block_size, Hkv, D] (model_runner.py:285-364 of the reference).  With
-        the head-major layout the storage is [2, layers, blocks, Hkv,
-        block_size, D] and this is a permuted view of it: every consumer
-        (store, attention) addresses pages through their strides."""
+        the head-major layout the storage is [layers, blocks, Hkv, 2,
+        block_size, D] -- one kv head's K rows and then its V rows, each a
+        contiguous run -- and this is a permuted view of it: every consumer
+        (store, attention) addresses pages through their strides, and a
+        layer's K and V views share them."""
         if self.config.kv_cache_layout == "head_major":
-            pages = torch.empty(kinds, layers, num_blocks, num_kv_heads, self.block_size, head_dim,
+            pages = torch.empty(layers, num_blocks, num_kv_heads, kinds, self.block_size, head_dim,
                                 dtype=dtype, device=self.device)
-            return pages.permute(0, 1, 2, 4, 3, 5)
+            return pages.permute(3, 0, 1, 4, 2, 5)
         return torch.empty(kinds, layers, num_blocks, self.block_size, num_kv_heads, head_dim,
                            dtype=dtype, device=self.device)
 

@@ -275,7 +275,13 @@ def _run_verify(K, cuda, case, fp8=False, head_major=False):
     if fp8:
         kc = kc.float().to(torch.float8_e4m3fn)
         vc = vc.float().to(torch.float8_e4m3fn)
-    if head_major:
+    if head_major == "kv_adjacent":
+        # the engine's pages: [blocks, Hkv, 2, block_size, D] (a head's K rows
+        # then its V rows), K and V seen as [blocks, block_size, Hkv, D]
+        both = torch.stack([kc.permute(0, 2, 1, 3), vc.permute(0, 2, 1, 3)], 2).contiguous()
+        both = both.to(cuda).permute(2, 0, 3, 1, 4)
+        dkc, dvc = both[0], both[1]
+    elif head_major:
         # pages stored [blocks, Hkv, block_size, D], seen as [blocks, block_size, Hkv, D]
         dkc = kc.permute(0, 2, 1, 3).contiguous().to(cuda).permute(0, 2, 1, 3)
         dvc = vc.permute(0, 2, 1, 3).contiguous().to(cuda).permute(0, 2, 1, 3)
@@ -322,18 +328,20 @@ def test_verify_attention_fp8(K, cuda):
     assert err <= ATTN_TOL, err
 
 
+@pytest.mark.parametrize("pages", ["head_major", "kv_adjacent"])
 @pytest.mark.parametrize("fp8", [False, True])
 @pytest.mark.parametrize("name,kw", [
     ("config3", dict(seed=8, batch=16, q_len=6, ctx_lo=256, ctx_hi=2304, hq=32, hkv=8)),
     ("decode", dict(seed=9, batch=12, q_len=1, ctx_lo=1, ctx_hi=1200, hq=32, hkv=8)),
     ("gqa8_k7", dict(seed=10, batch=3, q_len=8, ctx_lo=8, ctx_hi=900, hq=64, hkv=8)),
 ])
-def test_verify_attention_head_major_pages(K, cuda, name, kw, fp8):
-    """The engine's head-major pages ([blocks, Hkv, block_size, D] storage):
-    the same store + attention through strided views."""
-    got, ref = _run_verify(K, cuda, paged_case(**kw), fp8=fp8, head_major=True)
+def test_verify_attention_head_major_pages(K, cuda, name, kw, fp8, pages):
+    """Head-major pages ([blocks, Hkv, block_size, D] storage, and the
+    engine's [blocks, Hkv, 2, block_size, D] with a head's K and V rows
+    adjacent): the same store + attention through strided views."""
+    got, ref = _run_verify(K, cuda, paged_case(**kw), fp8=fp8, head_major=pages)
     err = np.abs(got - ref).max()
-    assert err <= ATTN_TOL, (name, fp8, err)
+    assert err <= ATTN_TOL, (name, fp8, pages, err)
 
 
 def test_fp8_decode_reference_geometry(K, cuda):
