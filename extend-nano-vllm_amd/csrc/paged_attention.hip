@@ -12,10 +12,10 @@
 //     end and cut into one equal range per SIMD of the device, so every wave
 //     streams the same number of keys whatever the length mix;
 //   * fixed (everything else): one workgroup per (kv head, sequence, query
-//     tile, key split).  For bf16 tiles of up to 32 rows four waves share a
-//     1536-key split (wave w takes chunks w, w+4, ...) and fold their
+//     tile, key split).  For bf16 tiles of up to 32 rows eight waves share a
+//     3072-key split (wave w takes chunks w, w+8, ...) and fold their
 //     softmax states together in LDS; otherwise one wave runs a 768-key
-//     split.  Several workgroups are resident per CU.
+//     split.
 // A sequence covered by one segment gets bf16 output directly; otherwise
 // each segment writes a normalised fp32 partial plus its log-sum-exp and
 // combine_kernel merges them.
@@ -59,11 +59,10 @@ constexpr int kChunk = 32;
 constexpr int kVPitch = 68;                          // dwords per staged V row
 constexpr int kVStage = kChunk * kVPitch;            // dwords of the wave's V stage
 constexpr int kSplitKeys = 768;        // fixed decomposition, one wave per split
-constexpr int kSharedSplitKeys = 1536;  // fixed decomposition, several waves per split
+constexpr int kKeysPerSharedWave = 384; // fixed decomposition, several waves per split
 constexpr int kMinSplit = 128;
 constexpr int64_t kMinWaves = 1024;
 // a split spans at most kWave - 2 blocks; blocks hold at least kChunk tokens
-static_assert(kSharedSplitKeys / kChunk + 2 <= kWave, "default split must fit the smallest block");
 constexpr int kMaxSeqGroups = 8;        // stream mode: up to 8 * 64 sequences
 constexpr int kMinRangeChunks = 4;      // stream mode: at least 128 keys per range
 constexpr float kLog2e = 1.4426950408889634f;
@@ -789,19 +788,26 @@ int32_t choose_qtile(int32_t max_q, int32_t group) {
 }
 
 // Split length: 768 keys (three 256-token blocks) for one wave per split;
-// 1536 when several waves share a split (each wave then walks every
-// waves-th chunk of it), which halves the split-combine traffic while keeping
-// each wave's share of keys near the one-wave figure.  Both were measured on
-// the Qwen3-8B verify shape (24-row tiles, 64 sequences, ~1.5k keys).  The
-// length shrinks in 128-key steps (to a 128-key minimum) only while fewer
-// than kMinWaves waves would be launched.
+// 384 keys per wave when several waves share a split (3072 for eight, each
+// wave walking every eighth chunk), which keeps a wave's share of keys near
+// the one-wave figure while most verify sequences need a single split and
+// no combine.  Measured on the Qwen3-8B verify shape (24-row tiles, 64
+// sequences, ~1.2k keys, longest first): eight waves on 3072 keys 66.0 us
+// per call against four on 1536 68.6 us and one on 768 83 us.  The length
+// shrinks in 128-key steps (to a 128-key minimum) only while fewer than
+// kMinWaves waves would be launched, and is capped so that a split spans at
+// most kWave - 2 blocks of block_size tokens (the kernel holds one block id
+// per lane); block_size 0 (unknown: the workspace query) assumes the
+// smallest block, kChunk tokens, which bounds the split count from above.
 void choose_split(int32_t num_seqs, int32_t num_kv_heads, int32_t n_qtiles, int32_t max_k,
-                  int32_t waves, int32_t* split_len, int32_t* max_splits) {
+                  int32_t waves, int32_t block_size, int32_t* split_len, int32_t* max_splits) {
   const int64_t base = static_cast<int64_t>(num_seqs > 0 ? num_seqs : 1) *
                        (num_kv_heads > 0 ? num_kv_heads : 1) * (n_qtiles > 0 ? n_qtiles : 1) *
                        (waves > 0 ? waves : 1);
   const int32_t mk = max_k > 1 ? max_k : 1;
-  int32_t len = waves > 1 ? kSharedSplitKeys : kSplitKeys;
+  int32_t len = waves > 1 ? kKeysPerSharedWave * waves : kSplitKeys;
+  const int32_t span = (kWave - 2) * (block_size > 0 ? block_size : kChunk);
+  if (len > span) len = span / kMinSplit * kMinSplit;
   while (len > kMinSplit && base * ((mk + len - 1) / len) < kMinWaves) len -= kMinSplit;
   // NVA_ATTN_SPLIT_KEYS (a multiple of 128) fixes the split length for tuning
   static const int32_t forced = [] {
@@ -821,9 +827,9 @@ void choose_split(int32_t num_seqs, int32_t num_kv_heads, int32_t n_qtiles, int3
 // (Qwen3-0.6B/8B/32B verify and draft-decode shapes):
 //   * single-tile sequences of up to 16 rows, bf16: stream decomposition, one
 //     wave per SIMD, one chunk buffer;
-//   * up to 32 rows, bf16: fixed decomposition, one chunk buffer, four waves
-//     per workgroup sharing each split (their states merged in LDS), several
-//     workgroups per CU hiding each other's latency;
+//   * up to 32 rows, bf16: fixed decomposition, one chunk buffer, eight waves
+//     per workgroup sharing each split (their states merged in LDS), two
+//     waves per SIMD hiding each other's latency;
 //   * single-tile sequences of up to 32 rows, FP8: stream decomposition with
 //     the chunk loads issued one chunk ahead;
 //   * 64-row tiles: fixed decomposition with the loads one chunk ahead (one
@@ -846,10 +852,10 @@ bool pipelined(int nt, bool fp8) {
   return forced >= 0 ? forced == 1 : (nt >= 4 || fp8);
 }
 
-// Waves sharing one split of the fixed decomposition.  Four for bf16 tiles
-// of up to 32 rows without the one-chunk-ahead loads (their state leaves
-// registers for four waves per SIMD); one otherwise.  NVA_ATTN_WPS=1/2/4/8
-// overrides it for those tiles (tuning).
+// Waves sharing one split of the fixed decomposition.  Eight for bf16 tiles
+// of up to 32 rows without the one-chunk-ahead loads (two waves per SIMD;
+// the eight parked states fill most of the CU's LDS); one otherwise.
+// NVA_ATTN_WPS=1/2/4/8 overrides it for those tiles (tuning).
 int segment_waves(int nt, bool fp8) {
   if (fp8 || nt >= 4 || pipelined(nt, fp8)) return 1;
   static const int forced = [] {
@@ -857,7 +863,7 @@ int segment_waves(int nt, bool fp8) {
     const int f = v ? atoi(v) : 0;
     return (f == 1 || f == 2 || f == 4 || f == 8) ? f : 0;
   }();
-  return forced ? forced : 4;
+  return forced ? forced : 8;
 }
 
 int tile_mfmas(int32_t tile_rows) { return tile_rows <= 16 ? 1 : tile_rows <= 32 ? 2 : 4; }
@@ -901,8 +907,8 @@ size_t workspace_bytes(int32_t num_seqs, int32_t num_tokens, int32_t hq, int32_t
   const int nt = tile_mfmas(qtile * (hkv > 0 ? hq / hkv : 1));
   // either KV dtype: the larger split count of the two wave choices
   int32_t len, ms, ms_fp8;
-  choose_split(num_seqs, hkv, n_qtiles, max_k, segment_waves(nt, false), &len, &ms);
-  choose_split(num_seqs, hkv, n_qtiles, max_k, segment_waves(nt, true), &len, &ms_fp8);
+  choose_split(num_seqs, hkv, n_qtiles, max_k, segment_waves(nt, false), 0, &len, &ms);
+  choose_split(num_seqs, hkv, n_qtiles, max_k, segment_waves(nt, true), 0, &len, &ms_fp8);
   ms = ms_fp8 > ms ? ms_fp8 : ms;
   if (ms > 1) {
     const size_t slots = static_cast<size_t>(num_tokens) * hq * ms;
@@ -992,7 +998,7 @@ int run_attention(AttnParams& p, int kv_dtype, void* workspace, size_t workspace
     grid = dim3(p.hkv, stream_ranges_per_head(p.hkv), 1);
   } else {
     choose_split(p.num_seqs, p.hkv, p.n_qtiles, p.max_k, segment_waves(tile_mfmas(tile_rows), fp8),
-                 &p.split_len, &p.max_splits);
+                 p.block_size, &p.split_len, &p.max_splits);
     // the kernel keeps one block id per lane: a split may touch at most kWave blocks
     if (p.split_len / p.block_size + 2 > kWave) return NVA_ERR_UNSUPPORTED;
     grid = dim3(p.hkv, p.num_seqs, p.max_splits * p.n_qtiles);
