@@ -7,14 +7,14 @@
 // (NT = 1, 2, 4); a verify step (k+1 positions) is a single tile, a prefill
 // is many.  Each tile only walks the keys its last row can see.  Segments
 // come from one of two decompositions:
-//   * stream (single-tile sequences of at most 16 rows, or 32 with an FP8
-//     cache): per kv head the key chunks of all sequences are laid end to
-//     end and cut into one equal range per SIMD of the device, so every wave
-//     streams the same number of keys whatever the length mix;
+//   * stream (single-tile sequences of at most 32 rows over an FP8 cache):
+//     per kv head the key chunks of all sequences are laid end to end and
+//     cut into one equal range per SIMD of the device, so every wave streams
+//     the same number of keys whatever the length mix;
 //   * fixed (everything else): one workgroup per (kv head, sequence, query
 //     tile, key split).  For bf16 tiles of up to 32 rows eight waves share a
 //     3072-key split (wave w takes chunks w, w+8, ...) and fold their
-//     softmax states together in LDS; otherwise one wave runs a 768-key
+//     softmax states together in LDS; otherwise one wave runs a 3072-key
 //     split.
 // A sequence covered by one segment gets bf16 output directly; otherwise
 // each segment writes a normalised fp32 partial plus its log-sum-exp and
@@ -58,7 +58,7 @@ constexpr int kCombineThreads = kCombineWaves * kWave;
 constexpr int kChunk = 32;
 constexpr int kVPitch = 68;                          // dwords per staged V row
 constexpr int kVStage = kChunk * kVPitch;            // dwords of the wave's V stage
-constexpr int kSplitKeys = 768;        // fixed decomposition, one wave per split
+constexpr int kSplitKeys = 3072;       // fixed decomposition, one wave per split
 constexpr int kKeysPerSharedWave = 384; // fixed decomposition, several waves per split
 constexpr int kMinSplit = 128;
 constexpr int64_t kMinWaves = 1024;
@@ -787,18 +787,20 @@ int32_t choose_qtile(int32_t max_q, int32_t group) {
   return max_q < qtile ? (max_q > 0 ? max_q : 1) : qtile;
 }
 
-// Split length: 768 keys (three 256-token blocks) for one wave per split;
-// 384 keys per wave when several waves share a split (3072 for eight, each
-// wave walking every eighth chunk), which keeps a wave's share of keys near
-// the one-wave figure while most verify sequences need a single split and
-// no combine.  Measured on the Qwen3-8B verify shape (24-row tiles, 64
-// sequences, ~1.2k keys, longest first): eight waves on 3072 keys 66.0 us
-// per call against four on 1536 68.6 us and one on 768 83 us.  The length
-// shrinks in 128-key steps (to a 128-key minimum) only while fewer than
-// kMinWaves waves would be launched, and is capped so that a split spans at
-// most kWave - 2 blocks of block_size tokens (the kernel holds one block id
-// per lane); block_size 0 (unknown: the workspace query) assumes the
-// smallest block, kChunk tokens, which bounds the split count from above.
+// Split length: 384 keys per wave when several waves share a split (3072
+// for eight, each wave walking every eighth chunk), 3072 keys when one wave
+// runs it (64-row tiles, FP8 tiles beyond the stream decomposition): most
+// verify sequences then need a single split and no combine, and long ones
+// write few fp32 partials.  Measured on MI355X, longest-first batches:
+// Qwen3-8B verify (24-row tiles, ~1.2k keys) eight waves on 3072 keys
+// 66.0 us per call against four on 1536 68.6 us; Qwen3-32B verify (64-row
+// tiles, 2-8k keys) one wave on 3072 keys 543 us against 648 us on 768 and
+// 566 us on 4096.  The length shrinks in 128-key steps (to a 128-key
+// minimum) only while fewer than kMinWaves waves would be launched, and is
+// capped so that a split spans at most kWave - 2 blocks of block_size tokens
+// (the kernel holds one block id per lane); block_size 0 (unknown: the
+// workspace query) assumes the smallest block, kChunk tokens, which bounds
+// the split count from above.
 void choose_split(int32_t num_seqs, int32_t num_kv_heads, int32_t n_qtiles, int32_t max_k,
                   int32_t waves, int32_t block_size, int32_t* split_len, int32_t* max_splits) {
   const int64_t base = static_cast<int64_t>(num_seqs > 0 ? num_seqs : 1) *
@@ -824,17 +826,18 @@ void choose_split(int32_t num_seqs, int32_t num_kv_heads, int32_t n_qtiles, int3
 // of at most 32 rows (64-row tiles need the whole register file for the
 // fixed decomposition's state already).
 // Decomposition and pipelining per tile shape, from measurements on MI355X
-// (Qwen3-0.6B/8B/32B verify and draft-decode shapes):
-//   * single-tile sequences of up to 16 rows, bf16: stream decomposition, one
-//     wave per SIMD, one chunk buffer;
+// (Qwen3-0.6B/8B/32B verify and draft-decode shapes, longest-first batches):
 //   * up to 32 rows, bf16: fixed decomposition, one chunk buffer, eight waves
 //     per workgroup sharing each split (their states merged in LDS), two
-//     waves per SIMD hiding each other's latency;
+//     waves per SIMD hiding each other's latency.  This beat the stream
+//     decomposition for 4- and 10-row tiles too (draft decode 80.8 -> 70.7
+//     us, Qwen3-0.6B verify 74.4 -> 65.1 us);
 //   * single-tile sequences of up to 32 rows, FP8: stream decomposition with
-//     the chunk loads issued one chunk ahead;
+//     the chunk loads issued one chunk ahead (502 us against 573 us fixed);
 //   * 64-row tiles: fixed decomposition with the loads one chunk ahead (one
 //     wave per SIMD for 64 rows: no room for a second).
-// NVA_ATTN_STREAM=0/1 and NVA_ATTN_PIPE=0/1 override the choices (tuning).
+// NVA_ATTN_STREAM=0/1 (1: also bf16 tiles of up to 16 rows) and
+// NVA_ATTN_PIPE=0/1 override the choices (tuning).
 int env_choice(const char* name) {
   const char* v = getenv(name);
   return v ? (atoi(v) != 0) : -1;
@@ -843,8 +846,8 @@ int env_choice(const char* name) {
 bool stream_mode(int32_t num_seqs, int32_t max_q, int32_t qtile, int32_t group, bool fp8) {
   static const int forced = env_choice("NVA_ATTN_STREAM");
   if (forced == 0 || max_q > qtile || num_seqs > kMaxSeqGroups * kWave) return false;
-  if (forced == 1) return max_q * group <= 32;
-  return max_q * group <= (fp8 ? 32 : 16);
+  if (forced == 1) return max_q * group <= (fp8 ? 32 : 16);
+  return fp8 && max_q * group <= 32;
 }
 
 bool pipelined(int nt, bool fp8) {
@@ -893,12 +896,14 @@ int32_t stream_ranges_per_head(int32_t hkv) {
 }
 
 // Workspace for either KV dtype (the size query does not name one): the
-// larger of the stream and fixed layouts that could apply.
+// larger of the stream and fixed layouts that could apply to either.
 size_t workspace_bytes(int32_t num_seqs, int32_t num_tokens, int32_t hq, int32_t hkv, int32_t max_q,
                        int32_t max_k) {
   const int32_t qtile = choose_qtile(max_q, hkv > 0 ? hq / hkv : 1);
+  const int32_t group = hkv > 0 ? hq / hkv : 1;
   size_t bytes = 0;
-  if (stream_mode(num_seqs, max_q, qtile, hkv > 0 ? hq / hkv : 1, false)) {
+  if (stream_mode(num_seqs, max_q, qtile, group, false) ||
+      stream_mode(num_seqs, max_q, qtile, group, true)) {
     const size_t slots = static_cast<size_t>(num_tokens) * hq * stream_max_splits(max_k);
     bytes = slots * kD * sizeof(float) + slots * sizeof(float) +
             static_cast<size_t>(num_tokens) * sizeof(int32_t) + 512;

@@ -59,3 +59,20 @@ def test_host_side_argument_errors_without_gpu():
         _native.check(_native.NVA_ERR_ARG, "probe")
     with pytest.raises(_native.KernelError):
         _native.check(_native.NVA_ERR_LAUNCH, "probe")
+
+
+def test_attention_workspace_covers_every_layout():
+    """The workspace size query names no KV dtype, so it must cover the
+    largest layout either dtype can pick: for single-tile batches of 17-32
+    rows that is the FP8 stream decomposition (split count bound: one per 4
+    chunks of 32 keys, plus one), even when bf16 would run unsplit."""
+    lib = _native.load()
+    seqs, tokens, hq, hkv, max_q, max_k = 16, 96, 32, 8, 6, 2310
+    got = lib.nva_paged_attention_workspace_size(seqs, tokens, hq, hkv, 128, max_q, max_k)
+    chunks = -(-max_k // 32)
+    splits = (chunks + 3) // 4 + 1
+    slots = tokens * hq * splits
+    need = slots * 128 * 4 + slots * 4 + tokens * 4
+    assert got >= need, (got, need)
+    # a bf16-only shape: no split at all needs no workspace beyond zero
+    assert lib.nva_paged_attention_workspace_size(64, 384, 32, 8, 128, 6, 1024) >= 0
