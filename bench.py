@@ -39,15 +39,15 @@ HBM_PEAK_GBS = 8000.0
 DEFAULT_GEMM_TUNING = os.path.join(ROOT, "extend-nano-vllm_amd", "nanovllm_amd", "tuning",
                                    "gemm_mi355x_qwen3_8b_eagle3.csv")
 
-# HBM bytes per verify-attention call (attention kernel + split combine) on
-# this workload, from two rocprofv3 --pmc runs of `bench.py --attention-only`
-# (FETCH_SIZE, then WRITE_SIZE; KiB per dispatch, averaged over 363 calls),
-# scaled by what the same counters read for a 1 GiB device copy in the same
-# runs: FETCH_SIZE 524300 KiB (x2.0 to bytes read), WRITE_SIZE 1048576 KiB
-# (x1.0).  attention: FETCH 159189.6, WRITE 5844.1; combine: FETCH 1875.2,
-# WRITE 912.0.  Only quoted for the default workload, whose shapes it was
-# measured on.
-PMC_TRAFFIC_BYTES = int(((159189.6 + 1875.2) * 2.0 + (5844.1 + 912.0) * 1.0) * 1024)
+# HBM bytes per verify-attention call on this workload, from two rocprofv3
+# --pmc runs of `bench.py --attention-only` (FETCH_SIZE, then WRITE_SIZE;
+# KiB per dispatch, averaged over 363 calls), scaled by what the same
+# counters read for a 1 GiB device copy in the same runs: FETCH_SIZE 524300
+# KiB (x2.0 to bytes read), WRITE_SIZE 1048576 KiB (x1.0).  attention kernel:
+# FETCH 158694.1, WRITE 3072.0 (no sequence of this workload needs a second
+# split, so no combine kernel runs).  Only quoted for the default workload,
+# whose shapes it was measured on.
+PMC_TRAFFIC_BYTES = int((158694.1 * 2.0 + 3072.0 * 1.0) * 1024)
 PMC_WORKLOAD = dict(preset="qwen3-8b", batch=64, k=5, prompt_min=256, prompt_max=2048,
                     max_tokens=256, seed=2)
 METRIC = "accepted tok/s, Qwen3-8B EAGLE3 k=5 bs64; verify-attn HBM GB/s % of peak"
@@ -158,7 +158,8 @@ class AttnTimer:
         self.calls = []
         return {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
-                "kernel": "paged_attention_kernel + split combine_kernel (one verify-attention call)",
+                "kernel": "paged_attention_kernel (+ combine_kernel when a sequence is split): one "
+                          "verify-attention call",
                 "launches": launches, "mean_us": round(mean_ms * 1e3, 2),
                 "bytes_per_launch": int(mean_bytes)}
 

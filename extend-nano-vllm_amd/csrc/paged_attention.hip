@@ -1010,8 +1010,12 @@ int run_attention(AttnParams& p, int kv_dtype, void* workspace, size_t workspace
   }
   if (stream || p.max_splits > 1) {
     const size_t need = workspace_bytes(p.num_seqs, p.num_tokens, p.hq, p.hkv, p.max_q, p.max_k);
-    if (!workspace || workspace_bytes_ < need || !aligned16(workspace)) return NVA_ERR_WORKSPACE;
     const size_t slots = static_cast<size_t>(p.num_tokens) * p.hq * p.max_splits;
+    // the layout this launch writes: partials, log-sum-exps, split counts
+    const size_t used = slots * kD * sizeof(float) + slots * sizeof(float) +
+                        static_cast<size_t>(p.num_tokens) * sizeof(int32_t);
+    if (!workspace || workspace_bytes_ < need || workspace_bytes_ < used || !aligned16(workspace))
+      return NVA_ERR_WORKSPACE;
     p.ws_o = static_cast<float*>(workspace);
     p.ws_lse = p.ws_o + slots * kD;
     p.row_nsplit = reinterpret_cast<int32_t*>(p.ws_lse + slots);
