@@ -129,25 +129,55 @@ __device__ __forceinline__ bf16x8_t fp8x8_to_bf16(uint2 w) {
   return __builtin_bit_cast(bf16x8_t, r);
 }
 
+// Query rows and keys of sequence seq (any lane's own sequence).  The end
+// of the key range is one load from a selected pointer (cu_k + 1 or
+// seqlens), issued with the others before any value is used, so the
+// geometry costs one memory latency.
 __device__ __forceinline__ void seq_geometry(const AttnParams& p, int seq, int& q_start, int& q_len,
                                              int& L) {
+  int q0 = seq, q1 = seq + 1, k0 = 0;
+  const int k1 = (p.cu_k ? p.cu_k + 1 : p.seqlens)[seq];
   if (p.cu_q) {
-    q_start = p.cu_q[seq];
-    q_len = p.cu_q[seq + 1] - q_start;
-  } else {
-    q_start = seq;
-    q_len = 1;
+    q0 = p.cu_q[seq];
+    q1 = p.cu_q[seq + 1];
   }
+  if (p.cu_k) k0 = p.cu_k[seq];
+  q_start = q0;
+  q_len = q1 - q0;
   q_len = q_len > p.max_q ? p.max_q : q_len;
   if (q_start < 0 || q_start >= p.num_tokens) q_len = 0;
   else if (q_len > p.num_tokens - q_start) q_len = p.num_tokens - q_start;
-  L = p.cu_k ? p.cu_k[seq + 1] - p.cu_k[seq] : p.seqlens[seq];
+  L = k1 - k0;
   L = L > p.max_k ? p.max_k : L;
 }
 
+// seq_geometry for a wave-uniform seq: readfirstlane states the values'
+// uniformity, which the compiler cannot see through the pointer select, so
+// that they stay in scalar registers (a buffer descriptor built from them
+// would otherwise need a waterfall loop per load).
+__device__ __forceinline__ void seq_geometry_uniform(const AttnParams& p, int seq, int& q_start,
+                                                     int& q_len, int& L) {
+  seq_geometry(p, seq, q_start, q_len, L);
+  q_start = __builtin_amdgcn_readfirstlane(q_start);
+  q_len = __builtin_amdgcn_readfirstlane(q_len);
+  L = __builtin_amdgcn_readfirstlane(L);
+}
+
+// Block ids of the split that starts at key kv_begin, one per lane: lane i
+// holds logical block kv_begin / block_size + i (the host keeps a split
+// within kWave - 2 blocks; lanes past the split hold ids nobody reads).
+// Needs no sequence geometry, so the fixed kernel issues it together with
+// the geometry loads instead of after them.
+__device__ __forceinline__ int split_block_ids(const AttnParams& p, int seq, int kv_begin) {
+  const int col = kv_begin / p.block_size + static_cast<int>(threadIdx.x & (kWave - 1));
+  return col < p.bt_cols ? p.block_tables[static_cast<int64_t>(seq) * p.bt_stride + col] : -1;
+}
+
 // One segment of work: the query tile qt of sequence seq (all its rows
-// for kv head kvh) against keys [kv_begin, kv_end), which is split `split`
-// of the `nsplit` splits covering the keys the tile can see.  A single split
+// for kv head kvh; the sequence's rows start at q_start, it has q_len query
+// rows and L keys) against keys [kv_begin, kv_end), which is split `split`
+// of the `nsplit` splits covering the keys the tile can see.  lane_blk is
+// split_block_ids(p, seq, kv_begin).  A single split
 // writes the bf16 output; otherwise a normalised fp32 partial and its
 // log-sum-exp go to the workspace for combine_kernel.
 //
@@ -157,8 +187,10 @@ __device__ __forceinline__ void seq_geometry(const AttnParams& p, int seq, int& 
 template <int NT, bool FP8, bool PIPE, int WPS>
 __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vst, bf16x8_t* qst,
                                                const int kvh, const int seq, const int qt,
+                                               const int q_start, const int q_len, const int L,
                                                const int kv_begin, const int kv_end,
-                                               const int split, const int nsplit) {
+                                               const int split, const int nsplit,
+                                               const int lane_blk) {
   static_assert(WPS == 1 || !PIPE, "shared segments use the single-buffer loop");
   static_assert(WPS == 1 || (NT <= 2 && (8 * kWave * 4 + 2 * kWave) <= kVStage),
                 "a wave's parked state must fit one V stage per column tile");
@@ -168,8 +200,6 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
   const int m16 = lane & 15;
   uint32_t* const stage = vst + wv * kVStage;           // this wave's V stage
 
-  int q_start, q_len, L;
-  seq_geometry(p, seq, q_start, q_len, L);
   // this tile's query positions: j0 .. j0 + jn - 1 of the sequence
   const int j0 = qt * p.qtile;
   const int jn = (q_len - j0 < p.qtile) ? q_len - j0 : p.qtile;
@@ -184,33 +214,27 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
   }
   const float sl2 = p.scale_log2 * kscale;
 
-  // ---- query operands (kept in LDS in operand order: entry (nt, s) is
-  // one 16-byte vector per lane, read back conflict-free for every chunk so
-  // that they hold no registers across the loop) and causal limits
+  // ---- query operands, loaded here and parked in LDS (in operand order:
+  // entry (nt, s) is one 16-byte vector per lane, read back conflict-free
+  // for every chunk so that they hold no registers across the loop) once
+  // the first chunk's K/V loads are in flight; and the causal limits
+  // Padding columns (n >= rows) load row 0 and are zeroed when parked, so
+  // the loads are unconditional and nothing waits for them before the K/V
+  // loads go out.
   int lim[NT];
+  bf16x8_t qv[NT][4];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const int n = nt * 16 + m16;
-    bf16x8_t qv[4];
-    if (n < rows) {
-      const int j = j0 + n / p.group, hh = n % p.group;
-      const uint16_t* qp = p.q + static_cast<int64_t>(q_start + j) * p.q_row_stride +
-                           static_cast<int64_t>(kvh * p.group + hh) * p.q_head_stride;
+    const int nn = n < rows ? n : 0;
+    const int j = j0 + nn / p.group, hh = nn % p.group;
+    const uint16_t* qp = p.q + static_cast<int64_t>(q_start + j) * p.q_row_stride +
+                         static_cast<int64_t>(kvh * p.group + hh) * p.q_head_stride;
 #pragma unroll
-      for (int s = 0; s < 4; ++s) qv[s] = *reinterpret_cast<const bf16x8_t*>(qp + 32 * s + 8 * g);
-      const int c = L - q_len + j;
-      lim[nt] = c < L - 1 ? c : L - 1;
-    } else {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) qv[s] = bf16x8_t{0, 0, 0, 0, 0, 0, 0, 0};
-      lim[nt] = -1;
-    }
-    if (wv == 0) {
-#pragma unroll
-      for (int s = 0; s < 4; ++s) qst[(nt * 4 + s) * kWave + lane] = qv[s];
-    }
+    for (int s = 0; s < 4; ++s) qv[nt][s] = *reinterpret_cast<const bf16x8_t*>(qp + 32 * s + 8 * g);
+    const int c = L - q_len + j;
+    lim[nt] = n < rows ? (c < L - 1 ? c : L - 1) : -1;
   }
-  if constexpr (WPS > 1) __syncthreads(); else lds_wave_sync();
 
   float m_run[NT], l_run[NT];
   f32x4_t acc[NT][8];
@@ -223,16 +247,11 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
   }
 
   const int nchunks = (kv_end - kv_begin + kChunk - 1) / kChunk;
-  const int32_t* bt = p.block_tables + static_cast<int64_t>(seq) * p.bt_stride;
   constexpr int64_t esz = FP8 ? 1 : 2;
 
-  // Block ids of this split, one per lane (lane i holds logical block
-  // first_blk + i; a split spans at most kWave blocks): one load up front
-  // instead of a dependent load per chunk.
+  // lane i of lane_blk holds the id of logical block first_blk + i: one
+  // load for the split instead of a dependent load per chunk
   const int first_blk = kv_begin / p.block_size;
-  const int nblk = (kv_end - 1) / p.block_size - first_blk + 1;
-  int lane_blk = -1;
-  if (lane < nblk && first_blk + lane < p.bt_cols) lane_blk = bt[first_blk + lane];
 
   // Raw K/V registers of one 32-key chunk (bf16: K 2x4 and V 8 16-byte
   // vectors per lane; FP8: K 2x4 8-byte and V 4 16-byte vectors).
@@ -422,6 +441,21 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
     lds_wave_sync();
   };
 
+  // The wave's first chunk is requested before the query operands are
+  // parked, so its latency overlaps the parking and the barrier (a barrier
+  // waits for LDS operations only, not for outstanding loads).
+  Chunk ca;
+  if (PIPE || wv < nchunks) load_chunk(PIPE ? 0 : wv, ca);
+  __builtin_amdgcn_sched_barrier(0);
+  if (wv == 0) {
+    const bf16x8_t zero = {0, 0, 0, 0, 0, 0, 0, 0};
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) qst[(nt * 4 + s) * kWave + lane] = nt * 16 + m16 < rows ? qv[nt][s] : zero;
+  }
+  if constexpr (WPS > 1) __syncthreads(); else lds_wave_sync();
+
   // Two register buffers, unrolled by two so that no buffer is copied: the
   // loads of chunk c+1 are issued before chunk c is computed.  The
   // scheduling barriers keep the compiler from sinking them to their use.
@@ -429,8 +463,7 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
   // again, from L2) so the compiler's wait counts only ever wait for the
   // older buffer.
   if constexpr (PIPE) {
-    Chunk ca, cb;
-    load_chunk(0, ca);
+    Chunk cb;
     const int last = nchunks - 1;
     int c = 0;
     for (; c < last; c += 2) {
@@ -444,10 +477,9 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
     if (c == last) compute_chunk(ca);
   } else {
     // one buffer: other resident waves on the SIMD hide the latency
-    Chunk ca;
     for (int c = wv; c < nchunks; c += WPS) {
-      load_chunk(c, ca);
       compute_chunk(ca);
+      if (c + WPS < nchunks) load_chunk(c + WPS, ca);
     }
   }
 
@@ -620,22 +652,28 @@ paged_attention_kernel(AttnParams p) {
   const int seq = blockIdx.y;
   const int split = blockIdx.z % p.max_splits;
   const int qt = blockIdx.z / p.max_splits;
+  const int kv_begin = split * p.split_len;
+  const int lane_blk = split_block_ids(p, seq, kv_begin);
   int q_start, q_len, L;
-  seq_geometry(p, seq, q_start, q_len, L);
+  seq_geometry_uniform(p, seq, q_start, q_len, L);
   const int j0 = qt * p.qtile;
   const int jn = (q_len - j0 < p.qtile) ? q_len - j0 : p.qtile;
-  if (jn <= 0) return;
-  const int kv_limit = L - q_len + j0 + jn;
+  const int kv_limit = L - q_len + j0 + jn;  // meaningful when jn > 0
   const int nsplit = kv_limit > 0 ? (kv_limit + p.split_len - 1) / p.split_len : 0;
-  if (kvh == 0 && split == 0 && p.row_nsplit) note_rows(p, seq, qt, nsplit);
-  if (kv_limit <= 0) {
-    if (split == 0) zero_tile(p, kvh, seq, qt);
+  const bool note = kvh == 0 && split == 0 && p.row_nsplit;
+  // one branch on the whole geometry, so every geometry load is issued
+  // before the first wait
+  if (jn <= 0 || kv_begin >= kv_limit) {
+    if (jn > 0) {
+      if (note) note_rows(p, seq, qt, nsplit);
+      if (kv_limit <= 0 && split == 0) zero_tile(p, kvh, seq, qt);
+    }
     return;
   }
-  const int kv_begin = split * p.split_len;
-  if (kv_begin >= kv_limit) return;
+  if (note) note_rows(p, seq, qt, nsplit);
   const int kv_end = kv_begin + p.split_len < kv_limit ? kv_begin + p.split_len : kv_limit;
-  attend_segment<NT, FP8, PIPE, WPS>(p, vst, qst, kvh, seq, qt, kv_begin, kv_end, split, nsplit);
+  attend_segment<NT, FP8, PIPE, WPS>(p, vst, qst, kvh, seq, qt, q_start, q_len, L, kv_begin, kv_end,
+                                     split, nsplit, lane_blk);
 }
 
 // Balanced ("stream") decomposition for one query tile per sequence (verify
@@ -669,8 +707,12 @@ paged_attention_stream_kernel(AttnParams p) {
     carry += __shfl(v, kWave - 1, kWave);
   }
   lds_wave_sync();
-  const int total = carry;
-  auto incl_of = [&](int s) { return pre[s + 1]; };
+  // Every value that places a range is wave-uniform (a shuffle of one lane,
+  // LDS entries read at one address); readfirstlane says so, so that the
+  // K/V buffer descriptors built from them stay in scalar registers instead
+  // of needing a waterfall loop around every load.
+  const int total = __builtin_amdgcn_readfirstlane(carry);
+  auto incl_of = [&](int s) { return __builtin_amdgcn_readfirstlane(pre[s + 1]); };
   const int rc_even = (total + static_cast<int>(gridDim.y) - 1) / static_cast<int>(gridDim.y);
   int rc = rc_even > p.min_range_chunks ? rc_even : p.min_range_chunks;
   rc = rc < p.max_range_chunks ? rc : p.max_range_chunks;
@@ -704,7 +746,7 @@ paged_attention_stream_kernel(AttnParams p) {
     int s = 0, hi_s = p.num_seqs - 1;
     while (s < hi_s) {
       const int mid = (s + hi_s) >> 1;
-      if (pre[mid + 1] <= start) s = mid + 1; else hi_s = mid;
+      if (incl_of(mid) <= start) s = mid + 1; else hi_s = mid;
     }
     for (; s < p.num_seqs; ++s) {
       const int hi = incl_of(s);
@@ -714,13 +756,14 @@ paged_attention_stream_kernel(AttnParams p) {
       const int c0 = (start > lo ? start : lo) - lo;
       const int c1 = (end < hi ? end : hi) - lo;
       int q_start, q_len, L;
-      seq_geometry(p, s, q_start, q_len, L);
+      seq_geometry_uniform(p, s, q_start, q_len, L);
       const int kv_limit = L;
       const int kv_begin = c0 * kChunk;
       const int kv_end = c1 * kChunk < kv_limit ? c1 * kChunk : kv_limit;
       const int split = r - lo / rc;
       const int nsplit = (hi - 1) / rc - lo / rc + 1;
-      attend_segment<NT, FP8, PIPE, 1>(p, vst, qst, kvh, s, 0, kv_begin, kv_end, split, nsplit);
+      attend_segment<NT, FP8, PIPE, 1>(p, vst, qst, kvh, s, 0, q_start, q_len, L, kv_begin, kv_end,
+                                       split, nsplit, split_block_ids(p, s, kv_begin));
     }
   }
 }
