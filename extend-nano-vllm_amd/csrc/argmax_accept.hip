@@ -3,31 +3,53 @@
 // Two launches, no cross-workgroup synchronisation (device-scope fences are
 // L2 write-backs on a multi-XCD part, far too costly per block):
 //   1. argmax_partial_kernel, grid (chunks_per_row, rows), 256 threads: each
-//      block scans one vocab chunk of one row with 16-byte loads.  Each thread
-//      walks its elements in increasing index order keeping (ord, index) of
-//      the first maximum; the block merges the threads' results as 64-bit keys
+//      block reduces one 16384-element vocab chunk of one row to the 64-bit
+//      key
 //          key = ord16(value) << 32 | (0xFFFFFFFF - index)
-//      where ord16 maps bf16 bit patterns to unsigned integers in numeric
-//      order (-0 folded onto +0, every NaN above +inf), so the maximum key is
-//      the first index of the maximum with NaN as the maximum -- the rule of
-//      torch.argmax.  The block's key goes to partials[row][chunk].
+//      of its first maximum, where ord16 maps bf16 bit patterns to unsigned
+//      integers in numeric order (-0 and +0 equal, every NaN above +inf), so
+//      the maximum key over a row is its first maximum with NaN as the
+//      maximum -- the rule of torch.argmax.  The block's key goes to
+//      partials[row][chunk].  Each thread holds eight 16-byte vectors in
+//      registers and maps them to ord16 with packed 16-bit operations (two
+//      elements per instruction), keeping only the running maximum; after
+//      the block's maximum is known, the threads holding it scan their
+//      registers for its first index.  A chunk with a NaN, an odd-length
+//      tail or unaligned rows takes an element-by-element loop instead.
 //   2. argmax_finalize_kernel, one wave per sequence (or per row group when
-//      there is no accept scan): merges each row's chunk keys, writes the
-//      argmax, then lane 0 runs the accept scan of speculative.py:11-30.
+//      there is no accept scan): loads all of the sequence's chunk keys and
+//      next input ids at once (one per lane), merges each row's keys, writes
+//      the argmax, then runs the accept scan of speculative.py:11-30.
 #include "common.h"
 
 namespace nva {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kTargetBlocks = 2048;   // ~8 blocks per CU on 256 CUs
-constexpr int kMinChunk = 4096;       // elements; two 16-byte loads per thread
-constexpr int kRowsPerFinalizeWave = 4;
+constexpr int kVecsPerThread = 8;                               // 16-byte vectors in registers
+constexpr int kChunkElems = kThreads * kVecsPerThread * 8;      // 16384 elements per block
 
+typedef __attribute__((ext_vector_type(2))) unsigned short u16x2_t;
+typedef __attribute__((ext_vector_type(2))) short s16x2_t;
+
+// ord16: 0x8000 + magnitude for non-negative values, 0x8000 - magnitude for
+// negative ones (so -0 == +0 and -inf = 0x0080), every NaN 0xFFFF.  Every
+// element's key is therefore above 0, which stands for "no element".
 __device__ __forceinline__ uint32_t ord16(uint32_t b) {
   const uint32_t mag = b & 0x7FFFu;
-  const uint32_t o = (b & 0x8000u) ? (~b & 0xFFFFu) : (b | 0x8000u);
-  return mag > 0x7F80u ? 0xFFFFu : (mag == 0 ? 0x8000u : o);
+  if (mag > 0x7F80u) return 0xFFFFu;
+  return (b & 0x8000u) ? 0x8000u - mag : 0x8000u + mag;
+}
+
+// ord16 of the two bf16 values of a 32-bit word, without the NaN rule (the
+// caller routes chunks holding a NaN to the exact loop); also raises
+// mag_max to the word's magnitudes.  Packed 16-bit ops: sign mask s, then
+// (mag ^ s) - s is +-mag, and ^ 0x8000 adds 0x8000 modulo 2^16.
+__device__ __forceinline__ uint32_t ord16x2(uint32_t w, u16x2_t& mag_max) {
+  const u16x2_t s = __builtin_bit_cast(u16x2_t, __builtin_bit_cast(s16x2_t, w) >> 15);
+  const u16x2_t m = __builtin_bit_cast(u16x2_t, w & 0x7FFF7FFFu);
+  mag_max = __builtin_elementwise_max(mag_max, m);
+  return __builtin_bit_cast(uint32_t, (m ^ s) - s) ^ 0x80008000u;
 }
 
 __device__ __forceinline__ uint64_t make_key(uint32_t ord, uint32_t idx) {
@@ -48,6 +70,18 @@ __device__ __forceinline__ uint64_t wave_max(uint64_t v) {
   return v;
 }
 
+// block-wide maximum of a 64-bit key (every thread gets it)
+__device__ __forceinline__ uint64_t block_max64(uint64_t v, uint64_t* red) {
+  v = wave_max(v);
+  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = v;
+  __syncthreads();
+  uint64_t r = red[0];
+#pragma unroll
+  for (int i = 1; i < kThreads / kWave; ++i) r = umax64(r, red[i]);
+  __syncthreads();
+  return r;
+}
+
 // strictly greater keeps the earlier index: elements arrive in index order
 __device__ __forceinline__ void take(uint32_t b, uint32_t idx, uint32_t& best_ord,
                                      uint32_t& best_idx) {
@@ -57,60 +91,117 @@ __device__ __forceinline__ void take(uint32_t b, uint32_t idx, uint32_t& best_or
   best_idx = gt ? idx : best_idx;
 }
 
+// exact element-by-element reduction of rp[begin, end): thread t visits
+// t, t + 256, ... in increasing order
+__device__ uint64_t chunk_exact(const uint16_t* __restrict__ rp, int32_t begin, int32_t end,
+                                uint64_t* red) {
+  uint32_t best_ord = 0, best_idx = 0xFFFFFFFFu;
+  for (int32_t c = begin + static_cast<int32_t>(threadIdx.x); c < end; c += kThreads)
+    take(rp[c], static_cast<uint32_t>(c), best_ord, best_idx);
+  // threads that saw nothing keep key 0, below every real key
+  return block_max64(best_idx == 0xFFFFFFFFu ? 0 : make_key(best_ord, best_idx), red);
+}
+
 __global__ void __launch_bounds__(kThreads)
 argmax_partial_kernel(const uint16_t* __restrict__ logits, int64_t row_stride, int32_t vocab,
-                      int32_t chunk_elems, int32_t chunks, bool vec,
-                      uint64_t* __restrict__ partials) {
+                      int32_t chunks, bool vec, uint64_t* __restrict__ partials) {
   __shared__ uint64_t red[kThreads / kWave];
   const int32_t row = blockIdx.y;
   const int32_t chunk = blockIdx.x;
-  const int32_t begin = chunk * chunk_elems;
-  int32_t end = begin + chunk_elems;
-  end = end > vocab ? vocab : end;
+  const int32_t begin = chunk * kChunkElems;
+  const int32_t end = begin + kChunkElems < vocab ? begin + kChunkElems : vocab;
   const uint16_t* rp = logits + static_cast<int64_t>(row) * row_stride;
-  uint32_t best_ord = 0, best_idx = 0xFFFFFFFFu;
-  if (vec) {
-    // thread t owns vectors t, t+256, ...: within a thread indices increase
-    const int32_t nvec = (end - begin) / 8;
-    const uint4* vp = reinterpret_cast<const uint4*>(rp + begin);
-#pragma unroll 4
-    for (int32_t v = threadIdx.x; v < nvec; v += kThreads) {
-      const uint4 w = vp[v];
-      const uint32_t base = static_cast<uint32_t>(begin + v * 8);
-      const uint32_t d[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) take((d[e >> 1] >> ((e & 1) * 16)) & 0xFFFFu, base + e, best_ord, best_idx);
-    }
-    for (int32_t c = begin + nvec * 8 + threadIdx.x; c < end; c += kThreads)
-      take(rp[c], static_cast<uint32_t>(c), best_ord, best_idx);
+  const int tid = static_cast<int>(threadIdx.x);
+  uint64_t key;
+  if (!vec || ((end - begin) & 7) != 0) {
+    key = chunk_exact(rp, begin, end, red);
   } else {
-    for (int32_t c = begin + threadIdx.x; c < end; c += kThreads)
-      take(rp[c], static_cast<uint32_t>(c), best_ord, best_idx);
-  }
-  // threads that saw nothing keep key 0, below every real key
-  uint64_t key = best_idx == 0xFFFFFFFFu ? 0 : make_key(best_ord, best_idx);
-  key = wave_max(key);
-  if ((threadIdx.x & (kWave - 1)) == 0) red[threadIdx.x / kWave] = key;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    uint64_t k = red[0];
+    // ---- phase 1: the chunk's vectors into registers as packed ord16
+    // keys (vector tid + 256 i of the chunk in o[i]); loads past the
+    // chunk's vectors read zeros and are set to key 0 below
+    const int32_t nvec = (end - begin) >> 3;
+    const __amdgpu_buffer_rsrc_t rs = make_rsrc(rp + begin, nvec * 16);
+    uint32_t o[kVecsPerThread][4];
+    u16x2_t mag_max = {0, 0};
 #pragma unroll
-    for (int i = 1; i < kThreads / kWave; ++i) k = umax64(k, red[i]);
-    partials[static_cast<int64_t>(row) * chunks + chunk] = k;
+    for (int i = 0; i < kVecsPerThread; ++i) {
+      const uint4 w = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (tid + kThreads * i) * 16, 0, 0));
+      o[i][0] = ord16x2(w.x, mag_max);
+      o[i][1] = ord16x2(w.y, mag_max);
+      o[i][2] = ord16x2(w.z, mag_max);
+      o[i][3] = ord16x2(w.w, mag_max);
+    }
+    if (nvec < kThreads * kVecsPerThread) {
+#pragma unroll
+      for (int i = 0; i < kVecsPerThread; ++i)
+        if (tid + kThreads * i >= nvec) o[i][0] = o[i][1] = o[i][2] = o[i][3] = 0;
+    }
+    u16x2_t omax = {0, 0};
+#pragma unroll
+    for (int i = 0; i < kVecsPerThread; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) omax = __builtin_elementwise_max(omax, __builtin_bit_cast(u16x2_t, o[i][j]));
+    const uint32_t lmax = omax.x > omax.y ? omax.x : omax.y;
+    const uint32_t lmag = mag_max.x > mag_max.y ? mag_max.x : mag_max.y;
+    // ---- the block's maximum key and largest magnitude in one reduction
+    const uint64_t both = block_max64((static_cast<uint64_t>(lmag > 0x7F80u) << 32) | lmax, red);
+    if (both >> 32) {
+      key = chunk_exact(rp, begin, end, red);   // a NaN: the exact loop applies its rule
+    } else {
+      const uint32_t M = static_cast<uint32_t>(both);
+      // ---- phase 2: the first index holding M (threads that hold it scan
+      // their registers from the last element back, so the first match wins)
+      uint32_t first = 0xFFFFFFFFu;
+      if (lmax == M) {
+#pragma unroll
+        for (int i = kVecsPerThread - 1; i >= 0; --i) {
+#pragma unroll
+          for (int j = 3; j >= 0; --j) {
+            const uint32_t at = static_cast<uint32_t>(begin + (tid + kThreads * i) * 8 + 2 * j);
+            first = (o[i][j] >> 16) == M ? at + 1 : first;
+            first = (o[i][j] & 0xFFFFu) == M ? at : first;
+          }
+        }
+      }
+      // the smallest index is the largest (0xFFFFFFFF - index)
+      key = block_max64(first == 0xFFFFFFFFu ? 0 : make_key(M, first), red);
+    }
   }
+  if (tid == 0) partials[static_cast<int64_t>(row) * chunks + chunk] = key;
 }
 
-// merge one row's chunk keys across the wave -> argmax index
-__device__ __forceinline__ uint32_t merge_row(const uint64_t* __restrict__ partials, int32_t row,
-                                              int32_t chunks) {
-  uint64_t k = 0;
-  for (int32_t c = wave_lane(); c < chunks; c += kWave)
-    k = umax64(k, partials[static_cast<int64_t>(row) * chunks + c]);
-  k = wave_max(k);
-  return 0xFFFFFFFFu - static_cast<uint32_t>(k);
+// One pass of a wave over rows r0 .. r0 + rn - 1 of a contiguous run of
+// rows whose chunk keys start at `keys`: lane l holds key l of the pass
+// (row l / chunks) when a pass covers whole rows, else the lane-strided
+// maximum of one row's keys.  Returns the lane's key and sets its row.
+__device__ __forceinline__ uint64_t pass_keys(const uint64_t* __restrict__ keys, int32_t chunks,
+                                              int32_t r0, int32_t rn, int32_t& my_row) {
+  const int lane = wave_lane();
+  uint64_t mine = 0;
+  my_row = -1;
+  if (chunks <= kWave) {
+    if (lane < rn * chunks) {
+      mine = keys[static_cast<int64_t>(r0) * chunks + lane];
+      my_row = lane / chunks;
+    }
+  } else {
+    for (int32_t c = lane; c < chunks; c += kWave)
+      mine = umax64(mine, keys[static_cast<int64_t>(r0) * chunks + c]);
+    my_row = 0;
+  }
+  return mine;
 }
 
-// one wave per sequence: argmax of its rows, then the accept scan
+__host__ __device__ __forceinline__ int32_t rows_per_pass(int32_t chunks) {
+  return chunks <= kWave ? kWave / chunks : 1;
+}
+
+// one wave per sequence: argmax of its rows, then the accept scan.  The
+// sequence's rows are contiguous, so its chunk keys are one contiguous run;
+// each pass loads the keys of as many rows as the lanes hold and those
+// rows' next input ids together, so a verify sequence (q <= 64 / chunks
+// rows) waits for memory once instead of once per row.
 __global__ void __launch_bounds__(kWave)
 argmax_accept_finalize_kernel(const uint64_t* __restrict__ partials, int32_t chunks,
                               int32_t num_rows, const int32_t* __restrict__ cu_q, int32_t num_seqs,
@@ -118,28 +209,37 @@ argmax_accept_finalize_kernel(const uint64_t* __restrict__ partials, int32_t chu
                               int32_t* __restrict__ accept_len, int32_t* __restrict__ bonus) {
   const int32_t s = blockIdx.x;
   if (s >= num_seqs) return;
+  const int lane = wave_lane();
   int32_t start = cu_q[s];
   int32_t stop = cu_q[s + 1];
   start = start < 0 ? 0 : start;
   stop = stop > num_rows ? num_rows : stop;
   const int32_t q = stop - start;
   if (q <= 0) {
-    if (wave_lane() == 0) {
+    if (lane == 0) {
       accept_len[s] = 0;
       bonus[s] = -1;
     }
     return;
   }
-  // lane 0 tracks the scan while rows are merged in order
-  int32_t a = 0;
+  const uint64_t* keys = partials + static_cast<int64_t>(start) * chunks;
+  int32_t a = 0, bonus_tok = -1;
   bool open = true;
-  int32_t bonus_tok = -1;
-  for (int32_t j = 0; j < q; ++j) {
-    const uint32_t idx = merge_row(partials, start + j, chunks);
-    if (wave_lane() == 0) {
-      argmax32[start + j] = static_cast<int32_t>(idx);
+  const int32_t per_pass = rows_per_pass(chunks);
+  for (int32_t r0 = 0; r0 < q; r0 += per_pass) {
+    const int32_t rn = q - r0 < per_pass ? q - r0 : per_pass;
+    // lane j < rn holds the input token that row r0 + j's argmax must match
+    const int64_t next = (lane < rn && r0 + lane < q - 1) ? input_ids[start + 1 + r0 + lane] : -1;
+    int32_t my_row;
+    const uint64_t mine = pass_keys(keys, chunks, r0, rn, my_row);
+    for (int32_t j = 0; j < rn; ++j) {
+      const uint64_t k = wave_max(my_row == j ? mine : 0);
+      const uint32_t idx = 0xFFFFFFFFu - static_cast<uint32_t>(k);
+      const int32_t row = r0 + j;
+      if (lane == 0) argmax32[start + row] = static_cast<int32_t>(idx);
       if (open) {
-        if (j < q - 1 && input_ids[start + 1 + j] == static_cast<int64_t>(idx)) {
+        const int64_t want = __shfl(next, j, kWave);
+        if (row < q - 1 && want == static_cast<int64_t>(idx)) {
           ++a;
         } else {
           open = false;
@@ -148,55 +248,47 @@ argmax_accept_finalize_kernel(const uint64_t* __restrict__ partials, int32_t chu
       }
     }
   }
-  if (wave_lane() == 0) {
+  if (lane == 0) {
     accept_len[s] = a;
     bonus[s] = bonus_tok;
   }
 }
 
-// rows without an accept scan: each wave finalises kRowsPerFinalizeWave rows
+// rows without an accept scan: each wave finalises one pass of rows
+// (rows_per_pass(chunks) rows, their keys loaded together)
 __global__ void __launch_bounds__(kWave)
 argmax_rows_finalize_kernel(const uint64_t* __restrict__ partials, int32_t chunks,
                             int32_t num_rows, const int64_t* __restrict__ index_map,
                             int64_t* __restrict__ out64) {
-  for (int32_t i = 0; i < kRowsPerFinalizeWave; ++i) {
-    const int32_t row = blockIdx.x * kRowsPerFinalizeWave + i;
-    if (row >= num_rows) return;
-    const uint32_t idx = merge_row(partials, row, chunks);
-    if (wave_lane() == 0)
-      out64[row] = static_cast<int64_t>(idx) + (index_map ? index_map[idx] : 0);
+  const int32_t per_pass = rows_per_pass(chunks);
+  const int32_t r0 = blockIdx.x * per_pass;
+  if (r0 >= num_rows) return;
+  const int32_t rn = num_rows - r0 < per_pass ? num_rows - r0 : per_pass;
+  int32_t my_row;
+  const uint64_t mine = pass_keys(partials, chunks, r0, rn, my_row);
+  for (int32_t j = 0; j < rn; ++j) {
+    const uint64_t k = wave_max(my_row == j ? mine : 0);
+    const uint32_t idx = 0xFFFFFFFFu - static_cast<uint32_t>(k);
+    if (wave_lane() == 0) out64[r0 + j] = static_cast<int64_t>(idx) + (index_map ? index_map[idx] : 0);
   }
 }
 
-void choose_chunks(int32_t rows, int32_t vocab, int32_t* chunk_elems, int32_t* chunks) {
-  const int32_t rows1 = rows > 0 ? rows : 1;
-  int32_t by_target = (kTargetBlocks + rows1 - 1) / rows1;
-  int32_t by_size = (vocab + kMinChunk - 1) / kMinChunk;
-  if (by_size < 1) by_size = 1;
-  int32_t c = by_target < by_size ? by_target : by_size;
-  if (c < 1) c = 1;
-  int32_t ce = (vocab + c - 1) / c;
-  ce = (ce + 8 * kThreads - 1) / (8 * kThreads) * (8 * kThreads);
-  *chunk_elems = ce;
-  *chunks = (vocab + ce - 1) / ce;
-}
+// Chunks of kChunkElems elements per row.
+int32_t row_chunks(int32_t vocab) { return vocab > 0 ? (vocab + kChunkElems - 1) / kChunkElems : 1; }
 
 size_t workspace_bytes(int32_t rows, int32_t vocab) {
-  int32_t ce, c;
-  choose_chunks(rows, vocab, &ce, &c);
-  return static_cast<size_t>(rows) * c * sizeof(uint64_t) + 16;
+  return static_cast<size_t>(rows) * row_chunks(vocab) * sizeof(uint64_t) + 16;
 }
 
 int launch_partials(const void* logits, int64_t row_stride, int32_t vocab, int32_t rows,
                     void* ws, size_t ws_bytes, hipStream_t stream, int32_t* chunks_out) {
-  int32_t ce, c;
-  choose_chunks(rows, vocab, &ce, &c);
+  const int32_t c = row_chunks(vocab);
   if (!ws || ws_bytes < workspace_bytes(rows, vocab) || (reinterpret_cast<uintptr_t>(ws) & 7u))
     return NVA_ERR_WORKSPACE;
   const bool vec = aligned16(logits) && (row_stride % 8 == 0);
   dim3 grid(c, rows);
   argmax_partial_kernel<<<grid, kThreads, 0, stream>>>(static_cast<const uint16_t*>(logits),
-                                                       row_stride, vocab, ce, c, vec,
+                                                       row_stride, vocab, c, vec,
                                                        static_cast<uint64_t*>(ws));
   *chunks_out = c;
   return launch_status();
@@ -245,7 +337,8 @@ extern "C" int nva_argmax_rows(const void* logits, int64_t row_stride, int32_t v
   const int st = launch_partials(logits, row_stride, vocab, num_rows, workspace, workspace_bytes_,
                                  s, &chunks);
   if (st != NVA_OK) return st;
-  const int32_t waves = (num_rows + kRowsPerFinalizeWave - 1) / kRowsPerFinalizeWave;
+  const int32_t per_pass = rows_per_pass(chunks);
+  const int32_t waves = (num_rows + per_pass - 1) / per_pass;
   argmax_rows_finalize_kernel<<<waves, kWave, 0, s>>>(static_cast<const uint64_t*>(workspace),
                                                       chunks, num_rows, index_map, out);
   return launch_status();

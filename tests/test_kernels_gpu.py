@@ -158,6 +158,41 @@ def test_argmax_accept_graph_replay(K, cuda):
         torch.cuda.synchronize()
 
 
+@pytest.mark.parametrize("shape", ["many_chunks", "multi_pass"])
+def test_argmax_finalize_passes(K, cuda, shape):
+    """The finalize kernels load the chunk keys of as many rows as a wave's
+    lanes hold per pass: rows split into more than 64 chunks (one row per
+    pass, lane-strided keys), and sequences longer than one pass of several
+    rows with the accepted prefix running across pass boundaries."""
+    g = torch.Generator().manual_seed(21)
+    if shape == "many_chunks":
+        qs, vocab = [3, 1], 300000            # > 64 chunks of >= 4096 elements per row
+    else:
+        qs, vocab = [30, 27, 9, 30], 32768    # eight chunks per row: eight rows per pass
+    t = sum(qs)
+    logits = torch.randn(t, vocab, generator=g).to(torch.bfloat16)
+    cu = torch.tensor([0] + np.cumsum(qs).tolist(), dtype=torch.int32)
+    ref_am = oracle.argmax_bf16(bits(logits))
+    np.testing.assert_array_equal(ref_am, logits.argmax(-1).numpy())
+    ids = torch.randint(0, vocab, (t,), generator=g)
+    # accept every proposal up to a per-sequence row, then reject
+    stops = [2, 0, 8, 29][: len(qs)]
+    for i, q in enumerate(qs):
+        s = int(cu[i])
+        for j in range(min(stops[i], q - 1)):
+            ids[s + 1 + j] = int(ref_am[s + j])
+        if stops[i] < q - 1:
+            ids[s + 1 + stops[i]] = (int(ref_am[s + stops[i]]) + 1) % vocab
+    am, acc, bonus = K.argmax_accept(logits.to(cuda), cu.to(cuda), ids.to(cuda))
+    ra, rb = oracle.accept(cu.numpy(), ref_am, ids.numpy())
+    np.testing.assert_array_equal(am.cpu().numpy(), ref_am)
+    np.testing.assert_array_equal(acc.cpu().numpy(), ra)
+    np.testing.assert_array_equal(bonus.cpu().numpy(), rb)
+    assert ra.tolist() == [min(s_, q - 1) for s_, q in zip(stops, qs)]
+    out = K.argmax_rows(logits.to(cuda))
+    np.testing.assert_array_equal(out.cpu().numpy(), ref_am.astype(np.int64))
+
+
 def test_argmax_rows_with_index_map(K, cuda):
     g = torch.Generator().manual_seed(4)
     rows, vocab = 64, 32000
