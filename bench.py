@@ -44,10 +44,10 @@ DEFAULT_GEMM_TUNING = os.path.join(ROOT, "extend-nano-vllm_amd", "nanovllm_amd",
 # KiB per dispatch, averaged over 363 calls), scaled by what the same
 # counters read for a 1 GiB device copy in the same runs: FETCH_SIZE 524300
 # KiB (x2.0 to bytes read), WRITE_SIZE 1048576 KiB (x1.0).  attention kernel:
-# FETCH 158694.1, WRITE 3072.0 (no sequence of this workload needs a second
+# FETCH 158701.0, WRITE 3072.0 (no sequence of this workload needs a second
 # split, so no combine kernel runs).  Only quoted for the default workload,
 # whose shapes it was measured on.
-PMC_TRAFFIC_BYTES = int((158694.1 * 2.0 + 3072.0 * 1.0) * 1024)
+PMC_TRAFFIC_BYTES = int((158701.0 * 2.0 + 3072.0 * 1.0) * 1024)
 PMC_WORKLOAD = dict(preset="qwen3-8b", batch=64, k=5, prompt_min=256, prompt_max=2048,
                     max_tokens=256, seed=2)
 METRIC = "accepted tok/s, Qwen3-8B EAGLE3 k=5 bs64; verify-attn HBM GB/s % of peak"
@@ -164,13 +164,15 @@ class AttnTimer:
                 "bytes_per_launch": int(mean_bytes)}
 
 
-def cpu_baseline(batches, seconds):
-    """Reference host acceptance on CPU torch, bounded to ~``seconds``."""
+def cpu_baseline(batches, seconds, one_thread_seconds=5.0):
+    """Reference host acceptance on CPU torch, bounded to ~``seconds`` with
+    every core the process may use, then ~``one_thread_seconds`` on one."""
+    import statistics
+
     import torch
     from oracle import oracle
 
     cores = len(os.sched_getaffinity(0))
-    torch.set_num_threads(cores)
     model = "unknown"
     try:
         for line in open("/proc/cpuinfo"):
@@ -179,26 +181,40 @@ def cpu_baseline(batches, seconds):
                 break
     except OSError:
         pass
-    logits, cu, ids = batches[0]
-    for _ in range(2):
-        oracle.reference_cpu_acceptance(logits, cu, ids)
-    times, committed = [], 0
-    t_end = time.perf_counter() + seconds
-    i = 0
-    while time.perf_counter() < t_end or len(times) < 3:
-        logits, cu, ids = batches[i % len(batches)]
-        t0 = time.perf_counter()
-        _, _, c = oracle.reference_cpu_acceptance(logits, cu, ids)
-        times.append(time.perf_counter() - t0)
-        committed += c
-        i += 1
-    total = sum(times)
-    return {"value": round(committed / total, 1), "unit": "accepted tok/s (acceptance logic only)",
+
+    def timed(threads, budget):
+        torch.set_num_threads(threads)
+        logits, cu, ids = batches[0]
+        for _ in range(3):
+            oracle.reference_cpu_acceptance(logits, cu, ids)
+        times, committed = [], 0
+        t_end = time.perf_counter() + budget
+        i = 0
+        while time.perf_counter() < t_end or len(times) < 3:
+            logits, cu, ids = batches[i % len(batches)]
+            t0 = time.perf_counter()
+            _, _, c = oracle.reference_cpu_acceptance(logits, cu, ids)
+            times.append(time.perf_counter() - t0)
+            committed += c
+            i += 1
+        return times, committed
+
+    times, committed = timed(cores, seconds)
+    times1, committed1 = timed(1, one_thread_seconds)
+    torch.set_num_threads(cores)
+    logits, cu, _ = batches[0]
+    rows = logits.shape[0]
+    med, med1 = statistics.median(times), statistics.median(times1)
+    return {"value": round(committed / sum(times), 1), "unit": "accepted tok/s (acceptance logic only)",
             "cores": cores, "kind": "port",
-            "sample": f"{len(times)} verify batches of [{logits.shape[0]}, {logits.shape[1]}] bf16 "
+            "sample": f"{len(times)} verify batches of [{rows}, {logits.shape[1]}] bf16 "
                       f"logits from this run ({len(cu) - 1} sequences each), per-sequence "
                       f"argmax+tolist+verify_greedy_proposals, torch CPU with {cores} threads on "
-                      f"{model}; {total / len(times) * 1e3:.1f} ms per batch"}
+                      f"{model}; median {med * 1e3:.1f} ms per batch",
+            "median_ms_per_batch": round(med * 1e3, 2), "rows_per_s": round(rows / med, 1),
+            "one_thread": {"value": round(committed1 / sum(times1), 1), "batches": len(times1),
+                           "median_ms_per_batch": round(med1 * 1e3, 2),
+                           "rows_per_s": round(rows / med1, 1)}}
 
 
 def attention_only(args) -> None:
