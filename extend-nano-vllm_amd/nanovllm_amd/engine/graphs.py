@@ -133,10 +133,16 @@ class VerifyGraph(_GraphBase):
         """Host lists for the real sequences (token ids, first position and
         query length per sequence, block tables); the rest of the bucket is
         padding: q rows at positions 0.. with no cache blocks."""
-        bs, q, T = self.bs, self.q, self.T
         n = len(ids)
+        self.i64.fill("ids", list(ids) + [0] * (self.T - n))
+        self.i64.upload()
+        self.run_staged_ids(starts, qlens, bt_rows)
+
+    def run_staged_ids(self, starts, qlens, bt_rows) -> None:
+        """As run(), with the input ids already in the device view of the
+        ids field (written on the device, e.g. from the draft's proposals)."""
+        bs, q = self.bs, self.q
         b = len(starts)
-        self.i64.fill("ids", list(ids) + [0] * (T - n))
         self.i32.fill("start", list(starts) + [0] * (bs - b))
         self.i32.fill("qlen", list(qlens) + [q] * (bs - b))
         flat = []
@@ -144,7 +150,6 @@ class VerifyGraph(_GraphBase):
             flat.extend(row + [-1] * (self.max_blocks - len(row)))
         flat.extend([-1] * (self.max_blocks * (bs - b)))
         self.i32.fill("bt", flat)
-        self.i64.upload()
         self.i32.upload()
         self.graph.replay()
 

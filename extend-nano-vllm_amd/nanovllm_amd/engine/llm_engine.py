@@ -98,14 +98,20 @@ class LLMEngine:
         """One EAGLE3 decode step over ``seqs``; returns the committed count."""
         for seq in seqs:
             self.scheduler.reserve_speculation(seq)
-        proposals = self.model_runner.call("propose_eagle3_batch", seqs)
+        # the runner may enqueue the verify right behind the draft, so that
+        # the host's bookkeeping below overlaps the target forward
+        proposals = self.model_runner.call("propose_verify_eagle3_batch", seqs)
+        pipelined = proposals is not None
+        if not pipelined:
+            proposals = self.model_runner.call("propose_eagle3_batch", seqs)
         bases = []
         for seq, proposal in zip(seqs, proposals):
             bases.append(self.scheduler.begin_speculation(seq, proposal))
             # the tail token (the previous target output) is verified with the drafts
             seq.num_computed_tokens = bases[-1] - 1
         targets, accept_len, bonus = self.model_runner.call(
-            "verify_eagle3_batch_fused", seqs, [len(p) + 1 for p in proposals])
+            "collect_verify_eagle3_batch" if pipelined else "verify_eagle3_batch_fused",
+            seqs, [len(p) + 1 for p in proposals])
         commit_seqs, commit_tokens, commit_starts = [], [], []
         for seq, proposal, base, target, a, b in zip(seqs, proposals, bases, targets,
                                                      accept_len, bonus):

@@ -123,6 +123,13 @@ class ModelRunner:
         self.keep_verify_inputs = False
         self.use_verify_graph = True
         self.last_verify_inputs = None
+        # propose and verify enqueued back to back (propose_verify_eagle3_batch)
+        self.pipeline_verify = True
+        # tests: draft_override(seqs, tokens) may rewrite the device proposals
+        # tokens [k, bucket] in place before they are verified
+        self.draft_override = None
+        self._inflight_verify = None
+        self._proposal_host = torch.empty(0, dtype=torch.int64)
         # one pinned host buffer receives argmax + accept results each verify
         self._verify_host = torch.empty(1 << 16, dtype=torch.int32, pin_memory=True)
         self._verify_dev = torch.empty(1 << 16, dtype=torch.int32, device=self.device)
@@ -527,6 +534,96 @@ class ModelRunner:
         out_t, out_a, out_b = [None] * len(seqs), [0] * len(seqs), [0] * len(seqs)
         for pos, i in enumerate(order):
             out_t[i], out_a[i], out_b[i] = targets[pos], acc[pos], bonus[pos]
+        return out_t, out_a, out_b
+
+    @torch.inference_mode()
+    def propose_verify_eagle3_batch(self, seqs: list[Sequence]):
+        """Proposals and verification in one pass over the stream: the draft
+        graph runs, its tokens are copied to the host, and the verify graph
+        is enqueued behind them with its input ids composed on the device
+        (previous token, then the k proposals of each sequence), so the
+        target forward runs while the host records the proposals.  Returns
+        the proposals (as propose_eagle3_batch) and leaves the verify in
+        flight for collect_verify_eagle3_batch; returns None when the graphs
+        do not cover the step (ragged proposal counts near max_tokens, no
+        bucket, or graphs off), and the caller then proposes and verifies in
+        turn.  The block tables must not change in between (the drafts'
+        blocks are reserved before proposing, as in the reference)."""
+        assert self.eagle3_model is not None
+        k = self.speculative_config.num_speculative_tokens
+        b = len(seqs)
+        bs = bucket_for(b)
+        if (not self.pipeline_verify or not self._use_graphs() or not self.use_verify_graph
+                or self.keep_verify_inputs or bs is None or k < 1 or b == 0
+                or any(seq.max_tokens - seq.num_completion_tokens < k for seq in seqs)):
+            return None
+        lens = [len(seq) for seq in seqs]
+        pos = [[n - 1 + s for n in lens] for s in range(k - 1)]
+        slots = [[self._slot(seq, p) for seq, p in zip(seqs, row)] for row in pos]
+        ctx_lens = [[p + 1 for p in row] for row in pos]
+        state_rows = _pinned(self._state_rows(seqs), torch.int64).to(self.device, non_blocking=True)
+        pgraph = self._propose_graphs.get(bs)
+        if pgraph is None:
+            pgraph = self._propose_graphs[bs] = ProposeGraph(self, bs, k)
+        vgraph = self._verify_graphs.get(bs)
+        if vgraph is None:
+            vgraph = self._verify_graphs[bs] = VerifyGraph(self, bs, k + 1)
+        tokens = pgraph.run(state_rows, pos, slots, ctx_lens, [seq.block_table for seq in seqs])
+        if self.draft_override is not None:
+            self.draft_override(seqs, tokens)
+        if self._proposal_host.numel() < k * bs:
+            self._proposal_host = torch.empty(k * bs, dtype=torch.int64, pin_memory=True)
+        host = self._proposal_host[:k * bs]
+        host.copy_(tokens.reshape(-1), non_blocking=True)
+        proposed = torch.cuda.Event()
+        proposed.record()
+        # the verify batch runs longest sequence first (verify_eagle3_batch_fused)
+        order = sorted(range(b), key=lambda i: -lens[i])
+        order_d = _pinned(order, torch.int64).to(self.device, non_blocking=True)
+        last_d = _pinned([seqs[i].token_ids[-1] for i in order], torch.int64).to(
+            self.device, non_blocking=True)
+        q = k + 1
+        ids = vgraph.i64.dev_view("ids")
+        rows = ids[:b * q].view(b, q)
+        rows[:, 0].copy_(last_d)
+        rows[:, 1:].copy_(tokens[:, :b].index_select(1, order_d).t())
+        if b * q < ids.numel():
+            ids[b * q:].zero_()
+        vgraph.run_staged_ids([lens[i] - 1 for i in order], [q] * b,
+                              [seqs[i].block_table for i in order])
+        t_pad = vgraph.T
+        self._verify_host[:t_pad + 2 * bs].copy_(vgraph.out, non_blocking=True)
+        verified = torch.cuda.Event()
+        verified.record()
+        self._inflight_verify = (order, vgraph, verified, [seqs[i].seq_id for i in range(b)])
+        proposed.synchronize()
+        table = host.view(k, bs)[:, :b].tolist()
+        return [[table[s][i] for s in range(k)] for i in range(b)]
+
+    @torch.inference_mode()
+    def collect_verify_eagle3_batch(self, seqs: list[Sequence], num_input_tokens: list[int]):
+        """Results of the verify propose_verify_eagle3_batch enqueued, in the
+        form of verify_eagle3_batch_fused (the same sequences, in the same
+        order, each verifying its k proposals)."""
+        if self._inflight_verify is None:
+            raise RuntimeError("collect_verify_eagle3_batch needs propose_verify_eagle3_batch first")
+        order, vgraph, verified, ids = self._inflight_verify
+        self._inflight_verify = None
+        k = self.speculative_config.num_speculative_tokens
+        b = len(seqs)
+        if [seq.seq_id for seq in seqs] != ids or any(n != k + 1 for n in num_input_tokens):
+            raise RuntimeError("EAGLE3 verification metadata does not match the proposed batch")
+        verified.synchronize()
+        bs, q, t_pad = vgraph.bs, vgraph.q, vgraph.T
+        res = self._verify_host[:t_pad + 2 * bs].tolist()
+        cu = [i * q for i in range(b + 1)]
+        out_t, out_a, out_b = [None] * b, [0] * b, [0] * b
+        for p, i in enumerate(order):
+            out_t[i] = res[cu[p]:cu[p + 1]]
+            out_a[i] = res[t_pad + p]
+            out_b[i] = res[t_pad + bs + p]
+        self._pending_verify = (vgraph.aux, cu, {seqs[i].seq_id: p for p, i in enumerate(order)})
+        self._pending_graph = vgraph
         return out_t, out_a, out_b
 
     def _verify_fused(self, seqs: list[Sequence], num_input_tokens: list[int]):

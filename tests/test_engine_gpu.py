@@ -246,3 +246,55 @@ def test_fp8_kv_cache_spec_equals_target_greedy(dirs):
             assert_same_greedy_path(plain, p, a, b)
     finally:
         plain.exit()
+
+
+def test_pipelined_verify_with_oracle_drafts(dirs):
+    """Graph steps with the verify enqueued behind the draft (input ids
+    composed on the device): proposals rewritten on the device to the
+    target's own greedy continuation, corrupted at a few positions, must give
+    the target's greedy path with multi-token commits, as the sequential
+    propose-then-verify path does."""
+    ps = [prompts(1, seed=17, lo=240, hi=250)[0], prompts(1, seed=18, lo=20, hi=30)[0],
+          prompts(1, seed=19, lo=500, hi=510)[0], prompts(1, seed=20, lo=60, hi=70)[0]]
+    max_tokens = [41, 29, 33, 26]
+    plain = make_llm(dirs, spec=False)
+    try:
+        ref = [plain.generate([p], SamplingParams(temperature=0.0, max_tokens=m, ignore_eos=True),
+                              use_tqdm=False)[0]["token_ids"] for p, m in zip(ps, max_tokens)]
+    finally:
+        plain.exit()
+    full = {tuple(p): p + r for p, r in zip(ps, ref)}
+    calls = {"n": 0, "pipelined": 0}
+
+    def override(seqs, tokens):
+        calls["pipelined"] += 1
+        k = tokens.shape[0]
+        host = tokens.cpu()
+        for i, seq in enumerate(seqs):
+            seqfull = full[tuple(seq.prompt_token_ids)]
+            want = seqfull[len(seq):len(seq) + k]
+            calls["n"] += 1
+            for s_, tok in enumerate(want):
+                host[s_, i] = tok
+            if calls["n"] % 3 == 0 and k > 2:
+                host[2, i] = (int(host[2, i]) + 1) % 2048   # reject from the third draft on
+        tokens.copy_(host.to(tokens.device))
+
+    spec = make_llm(dirs, spec=True, k=5, eager=False)
+    spec.model_runner.draft_override = override
+    try:
+        for p, m in zip(ps, max_tokens):
+            spec.add_request(p, SamplingParams(temperature=0.0, max_tokens=m, ignore_eos=True))
+        outs = {}
+        while not spec.is_finished():
+            for seq_id, toks in spec.step()[0]:
+                outs[seq_id] = toks
+        got = [outs[i] for i in sorted(outs)]
+        for p, a, b in zip(ps, got, ref):
+            assert_same_greedy_path(spec, p, a, b)
+        stats = spec.spec_stats
+        assert calls["pipelined"] > 0
+        assert stats["accepted"] > stats["steps"]          # multi-token commits happened
+        assert stats["committed"] == sum(max_tokens) - len(ps)
+    finally:
+        spec.exit()
