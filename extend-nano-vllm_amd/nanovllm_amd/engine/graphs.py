@@ -14,6 +14,11 @@ eagerly; results are identical either way.
   CommitGraph   draft replay of n committed tokens per sequence, aux rows
                 gathered from the VerifyGraph's static aux states
                                                   (model_runner.py:1216-1249)
+  DeviceCommitGraph
+                the same replay with every sequence's committed tail read
+                from the VerifyGraph's own accept results on the device, so
+                it can run right behind the verify, before the host has
+                seen the results
 """
 from __future__ import annotations
 
@@ -276,4 +281,70 @@ class CommitGraph(_GraphBase):
         self.i32.fill("bt", flat)
         self.i64.upload()
         self.i32.upload()
+        self.graph.replay()
+
+
+class DeviceCommitGraph(_GraphBase):
+    """Draft replay of the committed tails of a VerifyGraph's batch, derived
+    on the device from that graph's results.  Sequence i (in the verify
+    batch's order) accepted a_i drafts, so it commits its verify rows
+    i*q .. i*q + a_i: the accepted drafts and then the bonus token, whose
+    ids are the target argmax of those rows (an accepted draft equals it),
+    at the rows' positions and slots.  Those are verify_metadata's outputs
+    for the verify starts and query lengths a_i + 1.  Every sequence of the
+    bucket commits, padding included (slot -1: no cache write; its state
+    goes to the runner's scratch state row), and finished sequences too
+    (their state row is released afterwards, their blocks were reserved),
+    so the graph needs nothing from the host but the state rows.  The draft
+    forward runs over all T = bs*q rows; rows past the committed ones have
+    position 0 and slot -1, and attention never reads them."""
+
+    def __init__(self, runner, verify: VerifyGraph):
+        super().__init__(runner)
+        self.verify = verify
+        self.bs, self.q, self.T = verify.bs, verify.q, verify.T
+        dev = self.device
+        self.i64 = _Staging({"state": self.bs}, torch.int64, dev)
+        self.i64.fill("state", [runner.scratch_state_row] * self.bs)
+        self.i64.upload()
+        self.t_idx = torch.arange(self.T, dtype=torch.int64, device=dev)
+        self.cu_q = torch.zeros(self.bs + 1, dtype=torch.int32, device=dev)
+        self.cu_k = torch.zeros(self.bs + 1, dtype=torch.int32, device=dev)
+        self.pos = torch.zeros(self.T, dtype=torch.int64, device=dev)
+        self.slots = torch.zeros(self.T, dtype=torch.int32, device=dev)
+        self._capture(self._body)
+
+    def _body(self):
+        r = self.runner
+        v = self.verify
+        draft = r.eagle3_model
+        bs, q, T = self.bs, self.q, self.T
+        bt = v.i32.dev_view("bt").view(bs, v.max_blocks)
+        start = v.i32.dev_view("start")
+        qlen = v.out[T:T + bs] + 1
+        K.verify_metadata(start, qlen, bt, r.block_size, T, self.cu_q, self.cu_k, self.pos,
+                          self.slots)
+        cu = self.cu_q.long()
+        seq = torch.searchsorted(cu[1:], self.t_idx, right=True)
+        seq_c = seq.clamp(max=bs - 1)
+        rows = seq_c * q + (self.t_idx - cu.index_select(0, seq_c))
+        rows = torch.where(seq < bs, rows, torch.full_like(rows, -1))
+        ids = v.out.index_select(0, rows.clamp(min=0)).long()
+        combined = draft.combine_hidden_states(aux_concat(v.aux, rows.to(torch.int32)))
+        set_context(True, self.cu_q, self.cu_k, q, r.max_seqlen_k, self.slots, None, bt)
+        try:
+            hidden, feedback = draft.forward_with_cache(ids, self.pos, combined)
+        finally:
+            reset_context()
+        last = cu[1:] - 1
+        state = self.i64.dev_view("state")
+        r.state_hidden.index_copy_(0, state, hidden.index_select(0, last))
+        r.state_feedback.index_copy_(0, state, feedback.index_select(0, last))
+
+    def run(self, state_rows) -> None:
+        """state_rows: the draft-state row of each sequence of the verify
+        batch, in its order."""
+        pad = self.bs - len(state_rows)
+        self.i64.fill("state", list(state_rows) + [self.runner.scratch_state_row] * pad)
+        self.i64.upload()
         self.graph.replay()

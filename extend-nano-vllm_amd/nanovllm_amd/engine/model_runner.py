@@ -26,7 +26,8 @@ from nanovllm_amd import _native
 from nanovllm_amd import kernels as K
 from nanovllm_amd.context import get_context, reset_context, set_context
 from nanovllm_amd.eagle3 import Eagle3KVCache, load_eagle3_model
-from nanovllm_amd.engine.graphs import CommitGraph, ProposeGraph, VerifyGraph, bucket_for
+from nanovllm_amd.engine.graphs import (CommitGraph, DeviceCommitGraph, ProposeGraph, VerifyGraph,
+                                        bucket_for)
 from nanovllm_amd.engine.sequence import Sequence
 from nanovllm_amd.layers import Attention, init_random_, param_bytes
 from nanovllm_amd.loader import load_model
@@ -91,6 +92,8 @@ class ModelRunner:
             self._verify_graphs: dict[int, VerifyGraph] = {}
             self._propose_graphs: dict[int, ProposeGraph] = {}
             self._commit_graphs: dict[tuple[int, int], CommitGraph] = {}
+            self._device_commit_graphs: dict[int, DeviceCommitGraph] = {}
+            self._device_committed = None
             self._pending_verify = None
             self._pending_graph = None
             if self.speculative_config is not None:
@@ -110,9 +113,11 @@ class ModelRunner:
             if self.eagle3_model is not None:
                 # recurrent draft state of every running sequence, one row each
                 h = self.eagle3_model.config.hidden_size
+                # plus one scratch row that padded graph rows write into
                 rows = config.max_num_seqs + 1
-                self.state_hidden = torch.zeros(rows, h, dtype=self.dtype, device=self.device)
-                self.state_feedback = torch.zeros(rows, h, dtype=self.dtype, device=self.device)
+                self.scratch_state_row = rows
+                self.state_hidden = torch.zeros(rows + 1, h, dtype=self.dtype, device=self.device)
+                self.state_feedback = torch.zeros(rows + 1, h, dtype=self.dtype, device=self.device)
                 self._state_slot: dict[int, int] = {}
                 self._free_state = list(range(rows - 1, -1, -1))
         finally:
@@ -123,8 +128,10 @@ class ModelRunner:
         self.keep_verify_inputs = False
         self.use_verify_graph = True
         self.last_verify_inputs = None
-        # propose and verify enqueued back to back (propose_verify_eagle3_batch)
+        # propose and verify enqueued back to back (propose_verify_eagle3_batch),
+        # and the draft commit right behind the verify (DeviceCommitGraph)
         self.pipeline_verify = True
+        self.device_commit = True
         # tests: draft_override(seqs, tokens) may rewrite the device proposals
         # tokens [k, bucket] in place before they are verified
         self.draft_override = None
@@ -176,6 +183,7 @@ class ModelRunner:
         self.eagle_graph_vars.clear()
         self._pending_graph = None
         self._commit_graphs.clear()
+        self._device_commit_graphs.clear()
         self._verify_graphs.clear()
         self._propose_graphs.clear()
 
@@ -595,6 +603,16 @@ class ModelRunner:
         self._verify_host[:t_pad + 2 * bs].copy_(vgraph.out, non_blocking=True)
         verified = torch.cuda.Event()
         verified.record()
+        self._device_committed = None
+        if self.device_commit:
+            # the draft commit follows on the device while the host works
+            # through the results (commit_eagle3_batch then has nothing to do)
+            cgraph = self._device_commit_graphs.get(bs)
+            if cgraph is None:
+                cgraph = self._device_commit_graphs[bs] = DeviceCommitGraph(self, vgraph)
+            state_rows = self._state_rows(seqs)
+            cgraph.run([state_rows[i] for i in order])
+            self._device_committed = vgraph
         self._inflight_verify = (order, vgraph, verified, [seqs[i].seq_id for i in range(b)])
         proposed.synchronize()
         table = host.view(k, bs)[:, :b].tolist()
@@ -630,6 +648,7 @@ class ModelRunner:
         k = self.speculative_config.num_speculative_tokens
         b = len(seqs)
         bs = bucket_for(b)
+        self._device_committed = None
         try:
             for seq, n in zip(seqs, num_input_tokens):
                 seq.num_scheduled_tokens = n
@@ -705,6 +724,10 @@ class ModelRunner:
         and one sequence at a time)."""
         if self._pending_verify is None:
             raise RuntimeError("commit_eagle3_batch needs a preceding verify")
+        if self._device_committed is not None and self._device_committed is self._pending_graph:
+            # DeviceCommitGraph already replayed every tail of this verify
+            self._device_committed = None
+            return
         aux, cu, index = self._pending_verify
         rows = []
         for seq, toks in zip(seqs, output_tokens):

@@ -298,3 +298,77 @@ def test_pipelined_verify_with_oracle_drafts(dirs):
         assert stats["committed"] == sum(max_tokens) - len(ps)
     finally:
         spec.exit()
+
+
+def test_device_commit_matches_host_commit(dirs):
+    """The draft commit derived on the device from the verify results (run
+    right behind the verify) leaves the same draft state as the commit built
+    from the host's accepted tails: after every step, each live sequence's
+    recurrent draft state agrees (the two replays run their GEMMs over
+    different row counts, so agreement is to bf16 rounding).  Drafts agree
+    with the target's greedy continuation for a varying number of steps, so
+    the committed tails have different lengths."""
+    ps = [prompts(1, seed=31 + i, lo=20 + 40 * i, hi=30 + 40 * i)[0] for i in range(5)]
+    sp = SamplingParams(temperature=0.0, max_tokens=24, ignore_eos=True)
+    plain = make_llm(dirs, spec=False)
+    try:
+        ref = [o["token_ids"] for o in plain.generate(ps, sp, use_tqdm=False)]
+    finally:
+        plain.exit()
+    full = {tuple(p): p + r for p, r in zip(ps, ref)}
+
+    def override(seqs, tokens):
+        # every proposal fixed: the target's next tokens for (len % 3 + 1)
+        # positions, then wrong ones, so acceptance does not depend on the
+        # draft state the two runs compute
+        host = tokens.cpu()
+        for i, seq in enumerate(seqs):
+            want = full[tuple(seq.prompt_token_ids)]
+            n = len(seq)
+            for s_ in range(tokens.shape[0]):
+                tok = want[n + s_] if n + s_ < len(want) else 0
+                host[s_, i] = tok if s_ <= n % 3 else (tok + 1) % 2048
+        tokens.copy_(host.to(tokens.device))
+
+    runs = {}
+    for device_commit in (True, False):
+        llm = make_llm(dirs, spec=True, k=4, eager=False)
+        llm.model_runner.device_commit = device_commit
+        llm.model_runner.draft_override = override
+        try:
+            for p in ps:
+                llm.add_request(p, sp)
+            states, outs = [], {}
+            while not llm.is_finished():
+                for seq_id, toks in llm.step()[0]:
+                    outs[seq_id] = toks
+                runner = llm.model_runner
+                snap = {}
+                for seq in llm.scheduler.running:
+                    row = runner._state_slot.get(seq.seq_id)
+                    if row is not None:
+                        snap[tuple(seq.prompt_token_ids)] = (
+                            len(seq), runner.state_hidden[row].float().cpu(),
+                            runner.state_feedback[row].float().cpu())
+                states.append(snap)
+            got = [outs[i] for i in sorted(outs)]
+            for p, g, r in zip(ps, got, ref):
+                assert_same_greedy_path(llm, p, g, r)
+            runs[device_commit] = (states, got, dict(llm.spec_stats))
+        finally:
+            llm.exit()
+    (sa_all, out_a, st_a), (sb_all, out_b, st_b) = runs[True], runs[False]
+    assert out_a == out_b
+    assert st_a["accepted"] == st_b["accepted"] > st_a["steps"]
+    assert len(sa_all) == len(sb_all) > 2
+    compared = 0
+    for sa, sb in zip(sa_all, sb_all):
+        assert sa.keys() == sb.keys()
+        for key in sa:
+            la, ha, fa = sa[key]
+            lb, hb, fb = sb[key]
+            assert la == lb
+            torch.testing.assert_close(ha, hb, atol=3e-2, rtol=3e-2)
+            torch.testing.assert_close(fa, fb, atol=3e-2, rtol=3e-2)
+            compared += 1
+    assert compared > 10
