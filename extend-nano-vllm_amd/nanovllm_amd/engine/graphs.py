@@ -22,6 +22,8 @@ eagerly; results are identical either way.
 """
 from __future__ import annotations
 
+import sys
+
 import torch
 
 from nanovllm_amd import kernels as K
@@ -76,11 +78,24 @@ class _GraphBase:
         self.graph = torch.cuda.CUDAGraph()
 
     def _capture(self, body) -> None:
-        """Eager run (allocates workspaces, compiles nothing), then capture."""
+        """Eager run (allocates workspaces, compiles nothing), then capture.
+
+        The capture begins outside inference mode: the first capture of a
+        process registers torch's CUDA generator and allocates its graph-safe
+        seed/offset tensors.  Allocated under inference mode they would be
+        inference tensors, and every later capture outside inference mode
+        (the caller's own graphs) would fail on their in-place update."""
         body()
         torch.cuda.synchronize(self.device)
-        with torch.cuda.graph(self.graph, pool=self.runner.graph_pool):
+        ctx = torch.cuda.graph(self.graph, pool=self.runner.graph_pool)
+        with torch.inference_mode(False):
+            ctx.__enter__()
+        try:
             body()
+        except BaseException:
+            ctx.__exit__(*sys.exc_info())
+            raise
+        ctx.__exit__(None, None, None)
         if self.runner.graph_pool is None:
             self.runner.graph_pool = self.graph.pool()
         torch.cuda.synchronize(self.device)

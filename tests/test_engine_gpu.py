@@ -198,6 +198,17 @@ def test_hip_graph_steps_are_greedy(dirs):
         assert caps["cuda_graph"] and caps["graph_batch_sizes"]
         for p, a, b in zip(ps, got, ref):
             assert_same_greedy_path(graphed, p, a, b)
+        # the engine's captures leave torch's generator usable by a caller's
+        # own capture outside inference mode while the engine's graphs live
+        x = torch.arange(8, dtype=torch.float32, device="cuda")
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            y = x * 2
+        for rep in range(3):
+            x.fill_(rep)
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(y.cpu(), torch.full((8,), 2.0 * rep))
     finally:
         graphed.exit()
 
