@@ -126,7 +126,8 @@ argmax_partial_kernel(const uint16_t* __restrict__ logits, int64_t row_stride, i
 #pragma unroll
     for (int i = 0; i < kVecsPerThread; ++i) {
       const uint4 w = __builtin_bit_cast(
-          uint4, __builtin_amdgcn_raw_buffer_load_b128(rs, (tid + kThreads * i) * 16, 0, 0));
+          uint4,
+          __builtin_amdgcn_raw_buffer_load_b128(rs, (tid + kThreads * i) * 16, 0, kLoadStreamed));
       o[i][0] = ord16x2(w.x, mag_max);
       o[i][1] = ord16x2(w.y, mag_max);
       o[i][2] = ord16x2(w.z, mag_max);

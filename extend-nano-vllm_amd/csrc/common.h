@@ -88,6 +88,11 @@ inline int launch_status() {
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Cache-policy operand of a buffer load that reads whole lines exactly once
+// (V pages, logits): the nt (non-temporal) bit, so streamed lines leave the
+// caches early and do not displace lines that are still to be re-read.
+constexpr int kLoadStreamed = 2;
+
 // Raw buffer descriptor over num_records bytes at base: loads at offsets
 // past the end return zeros (dword 3: 32-bit data format, no swizzle).
 constexpr int kRsrcWord3 = 0x00020000;
