@@ -495,10 +495,10 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
     // state, half per column tile: tile 0 in its own V stage (free once its
     // loop is done), tile 1 in a second bank of WPS stages that no loop
     // touches, so no barrier is needed before parking.  After one barrier
-    // wave w finishes head_dim columns 32 pp .. 32 pp + 31 for pp = w,
-    // w + WPS, ..., folding the WPS states in wave order (deterministic), and
-    // writes them straight from registers: lane (g, m16) holds 8 consecutive
-    // values of query column m16.
+    // the NT * 4 items (column tile nt, head_dim columns 32 pp .. 32 pp + 31)
+    // are dealt to the waves in turn; each folds the WPS states of its item
+    // in wave order (deterministic) and writes them straight from registers:
+    // lane (g, m16) holds 8 consecutive values of query column m16.
     constexpr int kAccWords = 8 * kWave * 4;
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
@@ -509,8 +509,10 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
       mine[kAccWords + kWave + lane] = l_run[nt];
     }
     __syncthreads();
-#pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
+    // NT * 4 (column tile, 32-wide head_dim group) items, one per wave
+    // where there are enough waves
+    for (int it = wv; it < NT * 4; it += WPS) {
+      const int nt = it / 4, pp = it % 4;
       const float* st[WPS];
       float fw[WPS];
       float M = -INFINITY;
@@ -535,36 +537,33 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
         const int tok = q_start + j;
         const int h = kvh * p.group + hh;
         const int64_t slot = (static_cast<int64_t>(tok) * p.hq + h) * p.max_splits + split;
+        // tiles 2 pp (even d) and 2 pp + 1 (odd d): d = 32 pp + 8 g + 2 i + e
+        float o[8];
 #pragma unroll
-        for (int pp = wv; pp < 4; pp += WPS) {
-          // tiles 2 pp (even d) and 2 pp + 1 (odd d): d = 32 pp + 8 g + 2 i + e
-          float o[8];
+        for (int e = 0; e < 2; ++e) {
+          f32x4_t sum = f32x4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int e = 0; e < 2; ++e) {
-            f32x4_t sum = f32x4_t{0.f, 0.f, 0.f, 0.f};
+          for (int w = 0; w < WPS; ++w) {
+            const f32x4_t a = reinterpret_cast<const f32x4_t*>(st[w])[(2 * pp + e) * kWave + lane];
 #pragma unroll
-            for (int w = 0; w < WPS; ++w) {
-              const f32x4_t a = reinterpret_cast<const f32x4_t*>(st[w])[(2 * pp + e) * kWave + lane];
-#pragma unroll
-              for (int i = 0; i < 4; ++i) sum[i] += fw[w] * a[i];
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) o[2 * i + e] = sum[i] * inv;
+            for (int i = 0; i < 4; ++i) sum[i] += fw[w] * a[i];
           }
-          const int d0 = 32 * pp + 8 * g;
-          if (nsplit == 1) {
-            uint16_t* op = p.out + static_cast<int64_t>(tok) * p.out_row_stride +
-                           static_cast<int64_t>(h) * p.out_head_stride + d0;
-            *reinterpret_cast<uint4*>(op) = make_uint4(pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]),
-                                                       pack_bf16(o[4], o[5]), pack_bf16(o[6], o[7]));
-          } else {
-            float* wo = p.ws_o + slot * kD + d0;
-            *reinterpret_cast<float4*>(wo) = make_float4(o[0], o[1], o[2], o[3]);
-            *reinterpret_cast<float4*>(wo + 4) = make_float4(o[4], o[5], o[6], o[7]);
-          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[2 * i + e] = sum[i] * inv;
         }
-        // log-sum-exp (log2 domain) of the column for combine_kernel
-        if (nsplit > 1 && wv == 0 && g == 0) p.ws_lse[slot] = lsum > 0.0f ? M + __log2f(lsum) : -INFINITY;
+        const int d0 = 32 * pp + 8 * g;
+        if (nsplit == 1) {
+          uint16_t* op = p.out + static_cast<int64_t>(tok) * p.out_row_stride +
+                         static_cast<int64_t>(h) * p.out_head_stride + d0;
+          *reinterpret_cast<uint4*>(op) = make_uint4(pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]),
+                                                     pack_bf16(o[4], o[5]), pack_bf16(o[6], o[7]));
+        } else {
+          float* wo = p.ws_o + slot * kD + d0;
+          *reinterpret_cast<float4*>(wo) = make_float4(o[0], o[1], o[2], o[3]);
+          *reinterpret_cast<float4*>(wo + 4) = make_float4(o[4], o[5], o[6], o[7]);
+          // log-sum-exp (log2 domain) of the column for combine_kernel
+          if (pp == 0 && g == 0) p.ws_lse[slot] = lsum > 0.0f ? M + __log2f(lsum) : -INFINITY;
+        }
       }
     }
     return;

@@ -52,8 +52,13 @@ SIGNATURES = {
                                           _P, _P, _P, _I64, _I64, _P, _SZ, _P]),
     "nva_rms_norm": (_INT, [_P, _I64, _P, _P, _I64, _I32, _I32, _F32, _P]),
     "nva_add_rms_norm": (_INT, [_P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _I32, _I32, _F32, _P]),
+    "nva_add_then_rms_norm": (_INT, [_P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _I32, _I32, _F32,
+                                     _P]),
     "nva_qk_norm_rope": (_INT, [_P, _I64, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32, _F32, _P,
                                 _P, _P]),
+    "nva_qk_norm_rope_store": (_INT, [_P, _I64, _P, _P, _P, _P, _I32, _I32, _I32, _I32, _I32,
+                                      _F32, _P, _P, _P, _INT, _I64, _I64, _I64, _I32, _I32, _P,
+                                      _P, _P, _P]),
     "nva_silu_mul": (_INT, [_P, _I64, _P, _I64, _I32, _I32, _P]),
     "nva_verify_metadata": (_INT, [_P, _P, _I32, _P, _I64, _I32, _I32, _P, _P, _P, _P, _I32, _P]),
 }

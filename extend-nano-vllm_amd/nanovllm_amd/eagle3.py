@@ -111,16 +111,26 @@ class Eagle3DecoderLayer(nn.Module):
     def forward(self, input_embeds, hidden_states, positions):
         """eagle3.py:128-146: attention over [norm(embed) | norm(hidden)], two
         residual adds."""
-        if self.norm_before_residual:
-            hidden_states = self.hidden_norm(hidden_states)
-            residual = hidden_states
-        else:
-            residual = hidden_states
-            hidden_states = self.hidden_norm(hidden_states)
-        attn_in = torch.cat((self.input_layernorm(input_embeds), hidden_states), dim=-1)
-        hidden_states = residual + self.self_attn(positions, attn_in)
-        residual = hidden_states
-        return residual + self.mlp(self.post_attention_layernorm(hidden_states))
+        mlp_out, residual = self.forward_parts(input_embeds, hidden_states, positions)
+        return residual + mlp_out
+
+    def forward_parts(self, input_embeds, hidden_states, positions):
+        """The layer up to its last residual add: returns (mlp_out, residual),
+        whose bf16 sum is the layer's output.  The two norms write straight
+        into the halves of the attention input (no concat), and the first
+        residual add is fused with post_attention_layernorm, which normalises
+        the bf16 sum exactly as the separate ops do."""
+        n, h = hidden_states.shape
+        attn_in = torch.empty(n, 2 * h, dtype=hidden_states.dtype, device=hidden_states.device)
+        K.rms_norm(input_embeds, self.input_layernorm.weight, self.input_layernorm.eps,
+                   out=attn_in[:, :h])
+        normed = K.rms_norm(hidden_states, self.hidden_norm.weight, self.hidden_norm.eps,
+                            out=attn_in[:, h:])
+        residual = normed if self.norm_before_residual else hidden_states
+        x, residual = K.add_then_rms_norm(self.self_attn(positions, attn_in), residual,
+                                          self.post_attention_layernorm.weight,
+                                          self.post_attention_layernorm.eps)
+        return self.mlp(x), residual
 
 
 class Eagle3ForCausalLM(nn.Module):
@@ -190,9 +200,11 @@ class Eagle3ForCausalLM(nn.Module):
             raise ValueError("EAGLE3 feedback hidden_states must have shape "
                              f"[num_tokens, {self.config.hidden_size}]")
         embeds = self.embed_tokens(input_ids)
-        for layer in self.layers:
+        for layer in self.layers[:-1]:
             hidden_states = layer(embeds, hidden_states, positions)
-        return self.norm(hidden_states), hidden_states
+        # the last layer's residual add is fused with the final norm
+        mlp_out, residual = self.layers[-1].forward_parts(embeds, hidden_states, positions)
+        return K.add_then_rms_norm(mlp_out, residual, self.norm.weight, self.norm.eps)
 
     def forward(self, input_ids, positions, target_hidden_states):
         return self.forward_with_cache(input_ids, positions,

@@ -464,6 +464,24 @@ def add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, 
     return out, res_out
 
 
+def add_then_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float):
+    """``h = x + residual`` in bf16, then RMSNorm(h) without residual, as the
+    EAGLE3 draft layer composes them (eagle3.py:141-146).  Returns
+    (normed, h); both are new tensors."""
+    lib = _native.load()
+    _require_cuda(x, residual, weight)
+    _rows2d(x, "x")
+    _rows2d(residual, "residual")
+    rows, h = x.shape
+    out = torch.empty(rows, h, dtype=BF16, device=x.device)
+    total = torch.empty(rows, h, dtype=BF16, device=x.device)
+    check(lib.nva_add_then_rms_norm(x.data_ptr(), x.stride(0), residual.data_ptr(),
+                                    residual.stride(0), weight.data_ptr(), out.data_ptr(),
+                                    out.stride(0), total.data_ptr(), total.stride(0), rows, h,
+                                    float(eps), _stream()), "add_then_rms_norm")
+    return out, total
+
+
 def qk_norm_rope(qkv: torch.Tensor, positions: torch.Tensor, q_norm_weight: torch.Tensor | None,
                  k_norm_weight: torch.Tensor | None, cos_sin: torch.Tensor, num_q_heads: int,
                  num_kv_heads: int, head_dim: int, eps: float):
@@ -484,6 +502,41 @@ def qk_norm_rope(qkv: torch.Tensor, positions: torch.Tensor, q_norm_weight: torc
                                cos_sin.shape[0], t, num_q_heads, num_kv_heads, head_dim,
                                float(eps), q.data_ptr(), k.data_ptr(), _stream()), "qk_norm_rope")
     return q, k
+
+
+def qk_norm_rope_store(qkv: torch.Tensor, positions: torch.Tensor,
+                       q_norm_weight: torch.Tensor | None, k_norm_weight: torch.Tensor | None,
+                       cos_sin: torch.Tensor, num_q_heads: int, num_kv_heads: int, head_dim: int,
+                       eps: float, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                       slot_mapping: torch.Tensor, k_scale: torch.Tensor | None = None,
+                       v_scale: torch.Tensor | None = None) -> torch.Tensor:
+    """qk_norm_rope, then store_kvcache of the rotated keys and the value
+    heads of ``qkv`` (models/qwen3.py:77-98; attention.py:189-217), in one
+    launch.  Returns q [T, Hq, D]; the cache contents are exactly those the
+    two separate calls leave."""
+    lib = _native.load()
+    _require_cuda(qkv, positions, q_norm_weight, k_norm_weight, cos_sin, k_cache, v_cache,
+                  slot_mapping)
+    _rows2d(qkv, "qkv")
+    if positions.dtype != torch.int64 or not positions.is_contiguous():
+        raise TypeError("positions must be contiguous int64")
+    if cos_sin.dtype != torch.float32 or not cos_sin.is_contiguous():
+        raise TypeError("cos_sin must be contiguous float32 [max_position, head_dim]")
+    kvd, bstr, tstr, hstr, nb, bs, c_hkv, c_d = _cache_args(k_cache, v_cache)
+    if (c_hkv, c_d) != (num_kv_heads, head_dim):
+        raise ValueError("cache heads / head_dim do not match the projection")
+    t = qkv.shape[0]
+    if slot_mapping.numel() != t:
+        raise ValueError("slot_mapping must have one entry per token")
+    _i32(slot_mapping, "slot_mapping")
+    q = torch.empty(t, num_q_heads, head_dim, dtype=BF16, device=qkv.device)
+    check(lib.nva_qk_norm_rope_store(
+        qkv.data_ptr(), qkv.stride(0), positions.data_ptr(), _ptr(q_norm_weight),
+        _ptr(k_norm_weight), cos_sin.data_ptr(), cos_sin.shape[0], t, num_q_heads, num_kv_heads,
+        head_dim, float(eps), q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), kvd, bstr,
+        tstr, hstr, nb, bs, slot_mapping.data_ptr(), _ptr(_scale(k_scale)),
+        _ptr(_scale(v_scale)), _stream()), "qk_norm_rope_store")
+    return q
 
 
 def silu_mul(x: torch.Tensor) -> torch.Tensor:

@@ -110,12 +110,22 @@ class Attention(nn.Module):
         ctx = get_context()
         if ctx.is_dummy:
             return torch.zeros_like(q)
+        self._check_bound(ctx)
+        K.store_kvcache(k, v, self.k_cache, self.v_cache, ctx.slot_mapping, self.k_scale,
+                        self.v_scale)
+        return self.attend(q)
+
+    def _check_bound(self, ctx) -> None:
         if not self.k_cache.numel():
             raise RuntimeError("attention needs a bound paged KV cache")
         if ctx.slot_mapping is None or ctx.block_tables is None:
             raise RuntimeError("paged KV attention requires slot mapping and block tables")
-        K.store_kvcache(k, v, self.k_cache, self.v_cache, ctx.slot_mapping, self.k_scale,
-                        self.v_scale)
+
+    def attend(self, q: torch.Tensor) -> torch.Tensor:
+        """The attention half of forward(): this step's K/V rows are already
+        in the cache (written by forward's store or by the fused
+        qk_norm_rope_store)."""
+        ctx = get_context()
         if ctx.is_prefill:
             return K.paged_attention_varlen(q, self.k_cache, self.v_cache, ctx.cu_seqlens_q,
                                             ctx.cu_seqlens_k, ctx.max_seqlen_q, ctx.max_seqlen_k,
@@ -159,6 +169,18 @@ class SelfAttention(nn.Module):
         qkv = self.qkv_proj(hidden_states)
         cos_sin = rope_cos_sin(self.head_dim, self.max_position, float(self.rope_theta),
                                qkv.device.index)
+        ctx = get_context()
+        attn = self.attn
+        if not ctx.is_dummy:
+            # norm + RoPE + this step's K/V write in one launch, then attention
+            attn._check_bound(ctx)
+            q = K.qk_norm_rope_store(qkv, positions,
+                                     self.q_norm.weight if self.use_qk_norm else None,
+                                     self.k_norm.weight if self.use_qk_norm else None,
+                                     cos_sin, self.num_heads, self.num_kv_heads, self.head_dim,
+                                     self.eps, attn.k_cache, attn.v_cache, ctx.slot_mapping,
+                                     attn.k_scale, attn.v_scale)
+            return self.o_proj(attn.attend(q).view(-1, self.q_size))
         q, k = K.qk_norm_rope(qkv, positions,
                               self.q_norm.weight if self.use_qk_norm else None,
                               self.k_norm.weight if self.use_qk_norm else None,

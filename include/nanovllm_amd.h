@@ -264,6 +264,18 @@ int nva_add_rms_norm(const void *x, int64_t x_row_stride, const void *residual,
                      int64_t out_row_stride, void *residual_out, int64_t residual_out_row_stride,
                      int32_t rows, int32_t hidden, float eps, void *stream);
 
+/* A bf16 tensor add followed by RMSNorm.forward without residual, as the
+ *   EAGLE3 draft layer composes them (nanovllm/models/eagle3.py:141-146, and
+ *   the final norm of forward_with_cache, :256-258):
+ *   sum_out = bf16(f32(x) + f32(residual));
+ *   out = bf16(bf16(sum_out * rsqrt(mean(sum_out^2) + eps)) * weight).
+ *   Differs from nva_add_rms_norm only in normalising the bf16-rounded sum.
+ *   sum_out must not be x or residual. */
+int nva_add_then_rms_norm(const void *x, int64_t x_row_stride, const void *residual,
+                          int64_t residual_row_stride, const void *weight, void *out,
+                          int64_t out_row_stride, void *sum_out, int64_t sum_out_row_stride,
+                          int32_t rows, int32_t hidden, float eps, void *stream);
+
 /* Qwen3Attention.project_qkv after the QKV GEMM (nanovllm/models/qwen3.py:
  *   77-98): per-head q/k RMSNorm (skipped when both norm weights are NULL,
  *   the EAGLE3 draft layer) then neox rotary embedding
@@ -276,6 +288,23 @@ int nva_qk_norm_rope(const void *qkv, int64_t row_stride, const int64_t *positio
                      int32_t max_position, int32_t num_tokens, int32_t num_q_heads,
                      int32_t num_kv_heads, int32_t head_dim, float eps, void *q_out, void *k_out,
                      void *stream);
+
+/* nva_qk_norm_rope followed by the paged K/V write of the layer
+ *   (nanovllm/models/qwen3.py:77-98 then store_kvcache,
+ *   nanovllm/layers/attention.py:189-217), in one launch: q_out as above;
+ *   the rotated key heads (rounded to bf16) and the value heads of qkv go to
+ *   the caches at slot_mapping[t] exactly as nva_store_kvcache_paged writes
+ *   them (same strides, kv_dtype, scales; a negative or out-of-range slot is
+ *   skipped).  No key tensor is produced. */
+int nva_qk_norm_rope_store(const void *qkv, int64_t row_stride, const int64_t *positions,
+                           const void *q_norm_weight, const void *k_norm_weight,
+                           const float *cos_sin, int32_t max_position, int32_t num_tokens,
+                           int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, float eps,
+                           void *q_out, void *k_cache, void *v_cache, int kv_dtype,
+                           int64_t cache_block_stride, int64_t cache_token_stride,
+                           int64_t cache_head_stride, int32_t num_blocks, int32_t block_size,
+                           const int32_t *slot_mapping, const float *k_scale,
+                           const float *v_scale, void *stream);
 
 /* ---------------------------------------------------------------------
  * Verify-batch metadata on the device.

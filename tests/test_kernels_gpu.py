@@ -504,3 +504,184 @@ def test_verify_metadata_matches_oracle(K, cuda, num_seqs, seed):
     np.testing.assert_array_equal(o_cu_k.cpu().numpy(), cu_k)
     np.testing.assert_array_equal(o_pos.cpu().numpy(), pos)
     np.testing.assert_array_equal(o_slots.cpu().numpy(), slots)
+
+
+# ---------------------------------------------------------------- layer kernels + fused K2
+
+def _qk_norm_rope_reference(qkv, positions, qw, kw, cos_sin, hq, hkv, d, eps):
+    """CPU torch restatement of project_qkv's q/k RMSNorm and neox RoPE
+    (models/qwen3.py:77-98, layernorm.py:70-82, rotary_embedding.py:6-48).
+    Returns the rotated q, k and, for error bounds, |x1| + |x2| of each
+    rotated pair (the normed inputs, repeated on both halves)."""
+    t = qkv.shape[0]
+    q = qkv[:, :hq * d].reshape(t, hq, d)
+    k = qkv[:, hq * d:(hq + hkv) * d].reshape(t, hkv, d)
+
+    def norm(x, w):
+        if w is None:
+            return x
+        xf = x.float()
+        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+        return xf.to(torch.bfloat16) * w
+
+    def rope(x):
+        cs = cos_sin[positions.clamp(0, cos_sin.shape[0] - 1)].unsqueeze(1)
+        cos, sin = cs.chunk(2, dim=-1)
+        x1, x2 = torch.chunk(x.float(), 2, dim=-1)
+        mag = x1.abs() + x2.abs()
+        return (torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), -1).to(torch.bfloat16),
+                torch.cat((mag, mag), -1))
+
+    (rq, mq), (rk, mk) = rope(norm(q, qw)), rope(norm(k, kw))
+    return rq, rk, mq, mk
+
+
+def _layer_case(seed, t=160, hq=16, hkv=8, d=128):
+    from nanovllm_amd.layers import rope_cos_sin
+
+    g = torch.Generator().manual_seed(seed)
+    qkv = (torch.randn(t, (hq + 2 * hkv) * d, generator=g) * 2.0).to(torch.bfloat16)
+    positions = torch.randint(0, 4000, (t,), generator=g)
+    qw = (1.0 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16)
+    kw = (1.0 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16)
+    cos_sin = rope_cos_sin(d, 4096, 1e6, 0)
+    return g, qkv, positions, qw, kw, cos_sin
+
+
+@pytest.mark.parametrize("with_norm", [True, False])
+def test_qk_norm_rope_matches_reference_formulas(K, cuda, with_norm):
+    """The kernel's fp32 mean runs in a different summation order than
+    torch's, so a normed element may round to the neighbouring bf16 value;
+    the rotation then carries that one-ulp input difference (bounded by
+    2^-7 (|x1| + |x2|) of the pair) plus one ulp of its own rounding.
+    Nearly every element is identical."""
+    hq, hkv, d = 16, 8, 128
+    _, qkv, pos, qw, kw, cos_sin = _layer_case(31)
+    qw, kw = (qw, kw) if with_norm else (None, None)
+    q, k = K.qk_norm_rope(qkv.to(cuda), pos.to(cuda), None if qw is None else qw.to(cuda),
+                          None if kw is None else kw.to(cuda), cos_sin, hq, hkv, d, 1e-6)
+    rq, rk, mq, mk = _qk_norm_rope_reference(qkv, pos, qw, kw, cos_sin.cpu(), hq, hkv, d, 1e-6)
+    for got, ref, mag in ((q.cpu(), rq, mq), (k.cpu(), rk, mk)):
+        diff = (got.float() - ref.float()).abs()
+        bound = (ref.float().abs() + (mag if with_norm else 0.0)) * 2.0 ** -7 * 1.01
+        assert bool((diff <= bound + 1e-30).all()), float((diff - bound).max())
+        assert float((got == ref).float().mean()) > 0.99
+
+
+@pytest.mark.parametrize("layout", ["token_major", "head_major"])
+@pytest.mark.parametrize("fp8", [False, True])
+@pytest.mark.parametrize("with_norm", [True, False])
+def test_qk_norm_rope_store_matches_separate_kernels(K, cuda, layout, fp8, with_norm):
+    """The fused launch leaves q and both caches bit-identical to
+    qk_norm_rope followed by store_kvcache (negative and out-of-range slots
+    skipped, FP8 scales applied)."""
+    hq, hkv, d, nb, bs = 16, 8, 128, 12, 256
+    g, qkv, pos, qw, kw, cos_sin = _layer_case(33)
+    t = qkv.shape[0]
+    slots = torch.randperm(nb * bs, generator=g)[:t].to(torch.int32)
+    slots[::7] = -1
+    slots[3] = nb * bs + 5
+    cdt = torch.float8_e4m3fn if fp8 else torch.bfloat16
+    init = torch.randn(nb, bs, hkv, d, generator=g).to(cdt)
+
+    def cache():
+        if layout == "head_major":
+            return init.permute(0, 2, 1, 3).contiguous().to(cuda).permute(0, 2, 1, 3)
+        return init.clone().to(cuda)
+
+    ks = torch.tensor([0.75], device=cuda) if fp8 else None
+    vs = torch.tensor([1.5], device=cuda) if fp8 else None
+    dq, dpos, dslots = qkv.to(cuda), pos.to(cuda), slots.to(cuda)
+    dqw = qw.to(cuda) if with_norm else None
+    dkw = kw.to(cuda) if with_norm else None
+    kc1, vc1, kc2, vc2 = cache(), cache(), cache(), cache()
+    q1, k1 = K.qk_norm_rope(dq, dpos, dqw, dkw, cos_sin, hq, hkv, d, 1e-6)
+    K.store_kvcache(k1, dq[:, (hq + hkv) * d:].view(t, hkv, d), kc1, vc1, dslots, ks, vs)
+    q2 = K.qk_norm_rope_store(dq, dpos, dqw, dkw, cos_sin, hq, hkv, d, 1e-6, kc2, vc2, dslots,
+                              ks, vs)
+    torch.cuda.synchronize()
+    assert torch.equal(q1.view(torch.int16).cpu(), q2.view(torch.int16).cpu())
+    for a, b in ((kc1, kc2), (vc1, vc2)):
+        np.testing.assert_array_equal(bits(a.contiguous().cpu()), bits(b.contiguous().cpu()))
+    # the rows with a valid slot did change
+    changed = bits(kc2.contiguous().cpu()) != bits(init)
+    assert changed.any()
+
+
+def test_silu_mul_vector_path_matches_scalar_and_reference(K, cuda):
+    """16-byte vector path == element path (bit-exact); both within one bf16
+    ulp of torch's bf16(bf16(silu(a)) * b) (activation.py:11-14), whose exp
+    may round differently from the device's."""
+    g = torch.Generator().manual_seed(41)
+    rows, inter = 40, 1000
+    full = (torch.randn(rows, 2 * inter + 1, generator=g) * 3).to(torch.bfloat16).to(cuda)
+    x_vec = full[:, :2 * inter].contiguous()           # row stride 2000: vector path
+    x_scalar = full[:, :2 * inter]                      # row stride 2001: element path
+    assert torch.equal(x_vec, x_scalar)
+    y_vec, y_scalar = K.silu_mul(x_vec), K.silu_mul(x_scalar)
+    torch.cuda.synchronize()
+    assert torch.equal(y_vec.view(torch.int16), y_scalar.view(torch.int16))
+    a, b = x_vec.cpu()[:, :inter], x_vec.cpu()[:, inter:]
+    ref = torch.nn.functional.silu(a) * b
+    diff = (y_vec.cpu().float() - ref.float()).abs()
+    assert bool((diff <= ref.float().abs() * 2.0 ** -7 * 1.01 + 1e-30).all())
+    assert float((y_vec.cpu() == ref).float().mean()) > 0.99
+
+
+@pytest.mark.parametrize("add", [False, True])
+def test_rms_norm_matches_reference_formulas(K, cuda, add):
+    """rms_forward / add_rms_forward (layernorm.py:70-107): the fp32 (sum) row
+    is normalised, rounded to bf16, multiplied by the bf16 weight; the new
+    residual is bf16(x + residual) exactly."""
+    g = torch.Generator().manual_seed(43)
+    rows, h = 96, 4096
+    x = (torch.randn(rows, h, generator=g) * 2).to(torch.bfloat16)
+    r = torch.randn(rows, h, generator=g).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(h, generator=g)).to(torch.bfloat16)
+    s = x.float() + r.float() if add else x.float()
+    ref = (s * torch.rsqrt(s.pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16) * w
+    if add:
+        out, res = K.add_rms_norm(x.to(cuda), r.to(cuda), w.to(cuda), 1e-6)
+        assert torch.equal(res.cpu().view(torch.int16), s.to(torch.bfloat16).view(torch.int16))
+    else:
+        out = K.rms_norm(x.to(cuda), w.to(cuda), 1e-6)
+    got = out.cpu()
+    diff = (got.float() - ref.float()).abs()
+    assert bool((diff <= ref.float().abs() * 2.0 ** -7 * 1.01 + 1e-30).all())
+    assert float((got == ref).float().mean()) > 0.99
+
+
+def test_add_then_rms_norm_equals_add_followed_by_rms_norm(K, cuda):
+    """The EAGLE3 draft's fused residual add + norm is bit-identical to a bf16
+    tensor add followed by rms_norm (eagle3.py:141-146), also with a strided
+    residual (a half of the attention input) and on the element path."""
+    g = torch.Generator().manual_seed(45)
+    for rows, h in ((64, 4096), (7, 1000)):
+        x = (torch.randn(rows, h, generator=g) * 2).to(torch.bfloat16).to(cuda)
+        wide = torch.randn(rows, 2 * h, generator=g).to(torch.bfloat16).to(cuda)
+        r = wide[:, h:]
+        w = (1 + 0.1 * torch.randn(h, generator=g)).to(torch.bfloat16).to(cuda)
+        out, total = K.add_then_rms_norm(x, r, w, 1e-6)
+        ref_total = x + r
+        ref_out = K.rms_norm(ref_total, w, 1e-6)
+        torch.cuda.synchronize()
+        assert torch.equal(total.view(torch.int16), ref_total.view(torch.int16))
+        assert torch.equal(out.view(torch.int16), ref_out.view(torch.int16))
+        # and it is not the fp32-sum variant on these inputs
+        out32, _ = K.add_rms_norm(x, r, w, 1e-6)
+        assert not torch.equal(out32.view(torch.int16), out.view(torch.int16))
+
+
+def test_rms_norm_into_strided_halves(K, cuda):
+    """rms_norm writing into the halves of a [rows, 2H] buffer equals the
+    concatenation of two separate results (the draft's attention input)."""
+    g = torch.Generator().manual_seed(47)
+    a = torch.randn(64, 4096, generator=g).to(torch.bfloat16).to(cuda)
+    b = torch.randn(64, 4096, generator=g).to(torch.bfloat16).to(cuda)
+    w = (1 + 0.1 * torch.randn(4096, generator=g)).to(torch.bfloat16).to(cuda)
+    both = torch.empty(64, 8192, dtype=torch.bfloat16, device=cuda)
+    K.rms_norm(a, w, 1e-6, out=both[:, :4096])
+    K.rms_norm(b, w, 1e-6, out=both[:, 4096:])
+    ref = torch.cat((K.rms_norm(a, w, 1e-6), K.rms_norm(b, w, 1e-6)), -1)
+    torch.cuda.synchronize()
+    assert torch.equal(both.view(torch.int16), ref.view(torch.int16))
