@@ -43,12 +43,12 @@ DEFAULT_GEMM_TUNING = os.path.join(ROOT, "extend-nano-vllm_amd", "nanovllm_amd",
 # --pmc runs of `bench.py --attention-only` (FETCH_SIZE, then WRITE_SIZE;
 # KiB per dispatch, averaged over the 75 calls of `--attention-only
 # --roofline-repeats 2`), scaled by what the same counters read for a 1 GiB
-# device copy in the same runs: FETCH_SIZE 524302 KiB (x2.0 to bytes read),
-# WRITE_SIZE 1048576 KiB (x1.0).  attention kernel: FETCH 158681.1, WRITE
+# device copy in the same runs: FETCH_SIZE 524301 KiB (x2.0 to bytes read),
+# WRITE_SIZE 1048576 KiB (x1.0).  attention kernel: FETCH 158667.1, WRITE
 # 3072.0 (no sequence of this workload needs a second split, so no combine
 # kernel runs).  Only quoted for the default workload, whose shapes it was
 # measured on.
-PMC_TRAFFIC_BYTES = int((158681.1 * 2.0 + 3072.0 * 1.0) * 1024)
+PMC_TRAFFIC_BYTES = int((158667.1 * 2.0 + 3072.0 * 1.0) * 1024)
 PMC_WORKLOAD = dict(preset="qwen3-8b", batch=64, k=5, prompt_min=256, prompt_max=2048,
                     max_tokens=256, seed=2)
 METRIC = "accepted tok/s, Qwen3-8B EAGLE3 k=5 bs64; verify-attn HBM GB/s % of peak"
