@@ -86,3 +86,114 @@ def paged_case(seed: int, batch: int, q_len, ctx_lo: int, ctx_hi: int, hq: int, 
                 block_tables=bt, cu_q=cu_q, cu_k=cu_k, lens=torch.tensor(lens, dtype=torch.int32),
                 slot_mapping=torch.tensor(slots, dtype=torch.int32), q_lens=qs,
                 block_size=block_size)
+
+
+# ---------------------------------------------------------------- scheduler traces
+
+def scheduler_trace(Scheduler, Sequence, SamplingParams, scenario, inputs=None, seed=0):
+    """Drive a Scheduler through prefill and speculative (or plain) decode
+    steps in the order LLMEngine.step uses them (llm_engine.py:118-186 of the
+    reference): reserve_speculation for every sequence, begin_speculation
+    with k' = min(k, max_tokens - completion) proposals, num_computed =
+    base - 1, then postprocess_speculation with the accepted prefix and the
+    replacement token.  With ``inputs=None`` the tokens, proposals and
+    acceptance lengths are drawn from ``random.Random(seed)`` and recorded;
+    otherwise the recorded ones are replayed.  Returns (inputs, snapshots):
+    one snapshot of every sequence, the block manager and the queues after
+    each step.  Implementation-agnostic: the classes are passed in."""
+    import random
+    from types import SimpleNamespace
+
+    sc = scenario
+    spec = SimpleNamespace(num_speculative_tokens=sc["k"]) if sc["k"] else None
+    cfg = SimpleNamespace(max_num_seqs=sc["max_num_seqs"],
+                          max_num_batched_tokens=sc["max_num_batched_tokens"],
+                          enable_prefill_batching=sc["enable_prefill_batching"],
+                          speculative_config=spec, eos=sc["eos"],
+                          num_kvcache_blocks=sc["num_blocks"], kvcache_block_size=256,
+                          enable_prefix_caching=sc["prefix_caching"])
+    sched = Scheduler(cfg)
+    seqs = []
+    for req in sc["requests"]:
+        sp = SamplingParams(temperature=0.0 if sc["k"] else 1.0, max_tokens=req["max_tokens"],
+                            ignore_eos=req["ignore_eos"])
+        seq = Sequence(list(req["prompt"]), sp)
+        seqs.append(seq)
+        sched.add(seq)
+    index = {id(s): i for i, s in enumerate(seqs)}
+    rng = random.Random(seed)
+    record = inputs is None
+    inputs = [] if record else list(inputs)
+    eos, k = sc["eos"], sc["k"]
+
+    def tok():
+        return eos if rng.random() < sc["p_eos"] else rng.randrange(1000)
+
+    def snapshot(step_seqs, is_prefill):
+        bm = sched.block_manager
+        return {
+            "scheduled": [index[id(s)] for s in step_seqs],
+            "is_prefill": bool(is_prefill),
+            "seqs": [[s.status.name, len(s), s.num_computed_tokens, s.num_cached_tokens,
+                      list(s.block_table), s.num_completion_tokens, s.last_token] for s in seqs],
+            "waiting": [index[id(s)] for s in sched.waiting],
+            "running": [index[id(s)] for s in sched.running],
+            "free": list(bm.free_block_ids),
+            "used": sorted(bm.used_block_ids),
+            "blocks": [[b.block_id, b.ref_count, b.hash, bool(b.ready), len(b.token_ids)]
+                       for b in bm.blocks if b.ref_count],
+            "hash_to_block": sorted([h, i] for h, i in bm.hash_to_block_id.items()),
+            "bm_stats": dict(bm.stats),
+            "stats": dict(sched.stats),
+        }
+
+    snaps = []
+    step = 0
+    while not sched.is_finished() and step < sc["max_steps"]:
+        try:
+            step_seqs, is_prefill = _trace_step(sched, step, record, inputs, tok, rng, k)
+        except (RuntimeError, ValueError, AssertionError) as exc:
+            # the reference's own failure (e.g. blocks exhausted by a
+            # speculative reservation) ends the trace; the message is part
+            # of the contract
+            snaps.append({"error": f"{type(exc).__name__}: {exc}"})
+            break
+        snaps.append(snapshot(step_seqs, is_prefill))
+        step += 1
+    final = [list(s.token_ids) for s in seqs]
+    return inputs, snaps, final
+
+
+def _trace_step(sched, step, record, inputs, tok, rng, k):
+    """One engine step of scheduler_trace (see there)."""
+    step_seqs, is_prefill = sched.schedule()
+    if is_prefill or not k:
+        if record:
+            toks = [tok() for _ in step_seqs]
+            inputs.append({"tokens": toks})
+        else:
+            toks = inputs[step]["tokens"]
+        sched.postprocess(step_seqs, toks, is_prefill)
+    else:
+        for s in step_seqs:
+            sched.reserve_speculation(s)
+        if record:
+            props, acc, repl = [], [], []
+            for s in step_seqs:
+                n = min(k, s.max_tokens - s.num_completion_tokens)
+                props.append([tok() for _ in range(n)])
+                acc.append(rng.randint(0, n))
+                repl.append(tok())
+            inputs.append({"proposals": props, "accept": acc, "replacement": repl})
+        else:
+            props = inputs[step]["proposals"]
+            acc = inputs[step]["accept"]
+            repl = inputs[step]["replacement"]
+        bases = []
+        for s, p in zip(step_seqs, props):
+            base = sched.begin_speculation(s, list(p))
+            bases.append(base)
+            s.num_computed_tokens = base - 1
+        for s, p, base, a, r in zip(step_seqs, props, bases, acc, repl):
+            sched.postprocess_speculation(s, base, list(p[:a]), r)
+    return step_seqs, is_prefill

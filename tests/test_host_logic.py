@@ -337,3 +337,40 @@ def test_gemm_tuning_file_is_well_formed(tmp_path):
     model = write_qwen3_config(str(tmp_path / "m"), "tiny")
     with pytest.raises(ValueError, match="gemm_tuning_file"):
         Config(model, gemm_tuning_file=str(tmp_path / "missing.csv"))
+
+
+# ---------------------------------------------------------------- reference traces
+
+def _traces():
+    import json
+    import os
+
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                        "scheduler_traces.json")
+    with open(path) as f:
+        return json.load(f)
+
+
+@pytest.mark.parametrize("index", range(7))
+def test_scheduler_matches_reference_traces(index):
+    """Step-by-step states of the reference's own Scheduler / BlockManager /
+    Sequence (recorded by tests/golden/gen_scheduler_traces.py from
+    nanovllm/engine/{scheduler,block_manager,sequence}.py) driven through
+    chunked and batched prefill, speculative steps with accepted prefixes,
+    bonus tokens, EOS and max_tokens clipping, page crossings, prefix-cache
+    hits, decode preemption and pool exhaustion: this build's classes,
+    replaying the same inputs, must reach identical block tables, free-list
+    order, reference counts, block hashes, queues and errors after every
+    step."""
+    from helpers import scheduler_trace
+    from nanovllm_amd.engine.scheduler import Scheduler
+    from nanovllm_amd.engine.sequence import Sequence
+    from nanovllm_amd.sampling_params import SamplingParams
+
+    trace = _traces()[index]
+    _, snaps, final = scheduler_trace(Scheduler, Sequence, SamplingParams, trace["scenario"],
+                                      inputs=trace["inputs"])
+    assert len(snaps) == len(trace["snapshots"]), trace["scenario"]["name"]
+    for step, (got, want) in enumerate(zip(snaps, trace["snapshots"])):
+        assert got == want, f"{trace['scenario']['name']} step {step}"
+    assert final == trace["final_tokens"]
