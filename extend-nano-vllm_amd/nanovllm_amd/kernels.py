@@ -440,8 +440,12 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float,
     _require_cuda(x, weight, out)
     _rows2d(x, "x")
     rows, h = x.shape
+    if weight.numel() != h:
+        raise ValueError("weight must have one element per hidden column")
     if out is None:
         out = torch.empty(rows, h, dtype=BF16, device=x.device)
+    elif out.dtype != BF16 or out.dim() != 2 or tuple(out.shape) != (rows, h) or out.stride(1) != 1:
+        raise ValueError("out must be bf16 [rows, hidden] with unit last stride")
     check(lib.nva_rms_norm(x.data_ptr(), x.stride(0), weight.data_ptr(), out.data_ptr(),
                            out.stride(0), rows, h, float(eps), _stream()), "rms_norm")
     return out
@@ -455,6 +459,8 @@ def add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, 
     _require_cuda(x, residual, weight)
     _rows2d(x, "x")
     _rows2d(residual, "residual")
+    if residual.shape != x.shape or weight.numel() != x.shape[1]:
+        raise ValueError("residual must match x and weight its hidden size")
     rows, h = x.shape
     out = torch.empty(rows, h, dtype=BF16, device=x.device)
     res_out = torch.empty(rows, h, dtype=BF16, device=x.device)
@@ -462,6 +468,13 @@ def add_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, 
                                weight.data_ptr(), out.data_ptr(), out.stride(0), res_out.data_ptr(),
                                res_out.stride(0), rows, h, float(eps), _stream()), "add_rms_norm")
     return out, res_out
+
+
+def _qkv_rows(qkv: torch.Tensor, positions: torch.Tensor, hq: int, hkv: int, d: int) -> None:
+    if positions.numel() != qkv.shape[0]:
+        raise ValueError("positions must have one entry per qkv row")
+    if qkv.shape[1] < (hq + 2 * hkv) * d:
+        raise ValueError("qkv rows must hold [q heads | k heads | v heads]")
 
 
 def add_then_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Tensor, eps: float):
@@ -472,6 +485,8 @@ def add_then_rms_norm(x: torch.Tensor, residual: torch.Tensor, weight: torch.Ten
     _require_cuda(x, residual, weight)
     _rows2d(x, "x")
     _rows2d(residual, "residual")
+    if residual.shape != x.shape or weight.numel() != x.shape[1]:
+        raise ValueError("residual must match x and weight its hidden size")
     rows, h = x.shape
     out = torch.empty(rows, h, dtype=BF16, device=x.device)
     total = torch.empty(rows, h, dtype=BF16, device=x.device)
@@ -495,6 +510,7 @@ def qk_norm_rope(qkv: torch.Tensor, positions: torch.Tensor, q_norm_weight: torc
     if cos_sin.dtype != torch.float32 or not cos_sin.is_contiguous():
         raise TypeError("cos_sin must be contiguous float32 [max_position, head_dim]")
     t = qkv.shape[0]
+    _qkv_rows(qkv, positions, num_q_heads, num_kv_heads, head_dim)
     q = torch.empty(t, num_q_heads, head_dim, dtype=BF16, device=qkv.device)
     k = torch.empty(t, num_kv_heads, head_dim, dtype=BF16, device=qkv.device)
     check(lib.nva_qk_norm_rope(qkv.data_ptr(), qkv.stride(0), positions.data_ptr(),
@@ -526,6 +542,7 @@ def qk_norm_rope_store(qkv: torch.Tensor, positions: torch.Tensor,
     if (c_hkv, c_d) != (num_kv_heads, head_dim):
         raise ValueError("cache heads / head_dim do not match the projection")
     t = qkv.shape[0]
+    _qkv_rows(qkv, positions, num_q_heads, num_kv_heads, head_dim)
     if slot_mapping.numel() != t:
         raise ValueError("slot_mapping must have one entry per token")
     _i32(slot_mapping, "slot_mapping")
