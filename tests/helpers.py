@@ -197,3 +197,45 @@ def _trace_step(sched, step, record, inputs, tok, rng, k):
         for s, p, base, a, r in zip(step_seqs, props, bases, acc, repl):
             sched.postprocess_speculation(s, base, list(p[:a]), r)
     return step_seqs, is_prefill
+
+
+# ---------------------------------------------------------------- full-size device cases
+
+def device_paged_case(dev, seed, batch, q_len, ctx_lo, ctx_hi, hq, hkv, fp8=False,
+                      shared_frac=0.0, head_dim=128, block_size=256):
+    """A BASELINE-sized verify batch built on the device (too large for the
+    CPU oracle): lengths L_i ~ U[ctx_lo, ctx_hi] (the q_len new rows
+    included), shuffled physical blocks in the engine's page order
+    ([blocks, Hkv, 2, block_size, D]: a head's K rows then its V rows, seen
+    as [blocks, block_size, Hkv, D] views), and the first ``shared_frac`` of
+    every sequence's blocks taken from one shared prefix (the same physical
+    ids for every sequence).  Returns a dict of device tensors."""
+    import torch
+
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(ctx_lo, ctx_hi + 1, (batch,), generator=g).tolist()
+    nblk = [-(-L // block_size) for L in lens]
+    nshared = [int(n * shared_frac) for n in nblk]
+    prefix = max(nshared)
+    total = prefix + sum(n - s for n, s in zip(nblk, nshared))
+    perm = torch.randperm(total, generator=g)
+    shared_ids, own_ids = perm[:prefix], perm[prefix:]
+    bt = torch.full((batch, max(nblk)), -1, dtype=torch.int32)
+    off = 0
+    for i, (n, s) in enumerate(zip(nblk, nshared)):
+        bt[i, :s] = shared_ids[:s].to(torch.int32)
+        bt[i, s:n] = own_ids[off:off + n - s].to(torch.int32)
+        off += n - s
+    gd = torch.Generator(device=dev).manual_seed(seed)
+    pages = torch.empty(total, hkv, 2, block_size, head_dim, dtype=torch.bfloat16, device=dev)
+    pages.normal_(0.0, 0.5, generator=gd)
+    if fp8:
+        pages = pages.to(torch.float8_e4m3fn)
+    view = pages.permute(2, 0, 3, 1, 4)
+    t = batch * q_len
+    q = (torch.randn(t, hq, head_dim, generator=gd, device=dev) * 0.5).to(torch.bfloat16)
+    cu_q = torch.arange(0, t + 1, q_len, dtype=torch.int32)
+    cu_k = torch.tensor([0] + lens, dtype=torch.int64).cumsum(0).to(torch.int32)
+    return {"pages": pages, "k_cache": view[0], "v_cache": view[1], "q": q,
+            "cu_q": cu_q.to(dev), "cu_k": cu_k.to(dev), "lens": lens, "q_len": q_len,
+            "block_tables": bt.to(dev), "max_k": max(lens)}

@@ -688,3 +688,72 @@ def test_rms_norm_into_strided_halves(K, cuda):
     ref = torch.cat((K.rms_norm(a, w, 1e-6), K.rms_norm(b, w, 1e-6)), -1)
     torch.cuda.synchronize()
     assert torch.equal(both.view(torch.int16), ref.view(torch.int16))
+
+
+# ---------------------------------------------------------------- K1 at full BASELINE sizes
+
+FULL_CASES = {
+    # FP8 pages, B128, q5, 16/8 heads, L ~ U[4096, 16384]
+    "config4_fp8": dict(seed=3, batch=128, q_len=5, ctx_lo=4096, ctx_hi=16384, hq=16, hkv=8,
+                        fp8=True),
+    # B128, q8, 64/8 heads, L ~ U[2048, 8192], 30% shared prefix pages
+    "config5": dict(seed=4, batch=128, q_len=8, ctx_lo=2048, ctx_hi=8192, hq=64, hkv=8,
+                    shared_frac=0.3),
+}
+
+
+@pytest.mark.parametrize("name", list(FULL_CASES))
+def test_full_size_verify_matches_decode_rows(K, cuda, name):
+    """At the BASELINE configs' full sizes (too large for the CPU oracle):
+    every verify row equals the decode entry's row with context length
+    L_i - q_i + j + 1 on the same pages (the reference's config-4 comparator:
+    a verify row expanded into a paged decode row, attention.py:249-293),
+    although the two launches decompose the keys differently (stream ranges
+    or 3072-key splits with a combine, against per-row splits)."""
+    from helpers import device_paged_case
+
+    c = device_paged_case(cuda, **FULL_CASES[name])
+    q_len, lens = c["q_len"], c["lens"]
+    one = torch.ones(1, device=cuda) if FULL_CASES[name].get("fp8") else None
+    out = K.paged_attention_varlen(c["q"], c["k_cache"], c["v_cache"], c["cu_q"], c["cu_k"],
+                                   q_len, c["max_k"], 128 ** -0.5, c["block_tables"],
+                                   k_scale=one, v_scale=one)
+    ctx = torch.tensor([L - q_len + j + 1 for L in lens for j in range(q_len)],
+                       dtype=torch.int32, device=cuda)
+    rows_bt = c["block_tables"].repeat_interleave(q_len, dim=0).contiguous()
+    dec = K.paged_attention_decode(c["q"], c["k_cache"], c["v_cache"], ctx, rows_bt,
+                                   128 ** -0.5, max_seqlen_k=c["max_k"], k_scale=one,
+                                   v_scale=one)
+    torch.cuda.synchronize()
+    err = (out.float() - dec.float()).abs().max().item()
+    scale = dec.float().abs().max().item()
+    assert bool(torch.isfinite(out.float()).all()) and scale > 1e-3, (name, scale)
+    # the north star's 2e-2, and a few bf16 ulps of the output's own scale
+    assert err <= min(ATTN_TOL, 1e-2 * scale), (name, err, scale)
+
+
+@pytest.mark.parametrize("name", list(FULL_CASES))
+def test_full_size_verify_constant_values(K, cuda, name):
+    """Softmax weights sum to one: with every V row of kv head h equal to
+    one vector c_h, every output row of the heads sharing it is c_h, across
+    all splits, stream ranges and the combine, at full size."""
+    from helpers import device_paged_case
+
+    case = FULL_CASES[name]
+    c = device_paged_case(cuda, **case)
+    hkv = case["hkv"]
+    g = torch.Generator(device=cuda).manual_seed(77)
+    cvec = (torch.rand(hkv, 128, generator=g, device=cuda) - 0.5).to(torch.bfloat16)
+    if case.get("fp8"):
+        cvec = cvec.float().to(torch.float8_e4m3fn)
+    # pages [blocks, Hkv, 2, block_size, D]: V is index 1 of dim 2
+    c["pages"][:, :, 1] = cvec[None, :, None, :].to(c["pages"].dtype)
+    one = torch.ones(1, device=cuda) if case.get("fp8") else None
+    out = K.paged_attention_varlen(c["q"], c["k_cache"], c["v_cache"], c["cu_q"], c["cu_k"],
+                                   c["q_len"], c["max_k"], 128 ** -0.5, c["block_tables"],
+                                   k_scale=one, v_scale=one)
+    torch.cuda.synchronize()
+    group = case["hq"] // hkv
+    want = cvec.float().repeat_interleave(group, dim=0)          # [Hq, D]
+    err = (out.float() - want[None]).abs().max().item()
+    assert err <= 1e-2 * want.abs().max().item() + 1e-6, (name, err)
