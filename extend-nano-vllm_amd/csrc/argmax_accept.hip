@@ -20,6 +20,9 @@
 //      there is no accept scan): loads all of the sequence's chunk keys and
 //      next input ids at once (one per lane), merges each row's keys, writes
 //      the argmax, then runs the accept scan of speculative.py:11-30.
+#include <atomic>
+#include <mutex>
+
 #include "common.h"
 
 namespace nva {
@@ -277,6 +280,47 @@ argmax_rows_finalize_kernel(const uint64_t* __restrict__ partials, int32_t chunk
 // Chunks of kChunkElems elements per row.
 int32_t row_chunks(int32_t vocab) { return vocab > 0 ? (vocab + kChunkElems - 1) / kChunkElems : 1; }
 
+// ---- static scratch of the allocation-free entry point
+//
+// The chunk keys of nva_argmax_accept_static live in this array instead of a
+// caller workspace.  Each GPU the library runs on holds its own copy until
+// the process ends.  Host code never passes `scratch` itself to a kernel
+// (on the host that name is a stand-in, not a device address): the device
+// address comes from hipGetSymbolAddress, looked up once per device with
+// that device current, and is kept in g_scratch_ptr.
+// Two keys beyond the limit: the workspace check asks for 16 bytes of slack.
+static __device__ __align__(256) uint64_t scratch[NVA_ARGMAX_STATIC_KEYS + 2];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// Device address of `scratch` on the current device (looked up on the first
+// call per device).  The stream must belong to that device.
+int static_scratch(hipStream_t stream, void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return NVA_ERR_LAUNCH;
+  if (stream) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(stream, &sdev) != hipSuccess) return NVA_ERR_ARG;
+    if (sdev != dev) return NVA_ERR_ARG;
+  }
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    p = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (!p) {
+      if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) {
+        (void)hipGetLastError();   // do not leave the error for the next launch check
+        return NVA_ERR_LAUNCH;
+      }
+      g_scratch_ptr[dev].store(p, std::memory_order_release);
+    }
+  }
+  *out = p;
+  return NVA_OK;
+}
+
 size_t workspace_bytes(int32_t rows, int32_t vocab) {
   return static_cast<size_t>(rows) * row_chunks(vocab) * sizeof(uint64_t) + 16;
 }
@@ -305,16 +349,26 @@ extern "C" size_t nva_argmax_workspace_size(int32_t num_rows, int32_t num_seqs, 
   return workspace_bytes(num_rows, vocab);
 }
 
-extern "C" int nva_argmax_accept(const void* logits, int64_t row_stride, int32_t vocab,
-                                 const int32_t* cu_seqlens_q, int32_t num_seqs,
-                                 int32_t num_tokens, const int64_t* input_ids, int32_t* argmax,
-                                 int32_t* accept_len, int32_t* bonus, void* workspace,
-                                 size_t workspace_bytes_, void* stream) {
+namespace {
+
+int check_accept_args(const void* logits, int64_t row_stride, int32_t vocab,
+                      const int32_t* cu_seqlens_q, int32_t num_seqs, int32_t num_tokens,
+                      const int64_t* input_ids, const int32_t* argmax, const int32_t* accept_len,
+                      const int32_t* bonus) {
   if (vocab <= 0 || num_seqs < 0 || num_tokens < 0 || row_stride < vocab) return NVA_ERR_ARG;
   if (num_seqs == 0) return NVA_OK;
   if (!cu_seqlens_q || !accept_len || !bonus) return NVA_ERR_ARG;
   if (num_tokens > 0 && (!logits || !input_ids || !argmax)) return NVA_ERR_ARG;
-  hipStream_t s = static_cast<hipStream_t>(stream);
+  return NVA_OK;
+}
+
+// The two launches of nva_argmax_accept over the given chunk-key buffer
+// (arguments already checked, num_seqs > 0).
+int argmax_accept_launch(const void* logits, int64_t row_stride, int32_t vocab,
+                         const int32_t* cu_seqlens_q, int32_t num_seqs, int32_t num_tokens,
+                         const int64_t* input_ids, int32_t* argmax, int32_t* accept_len,
+                         int32_t* bonus, void* workspace, size_t workspace_bytes_,
+                         hipStream_t s) {
   int32_t chunks = 1;
   if (num_tokens > 0) {
     const int st = launch_partials(logits, row_stride, vocab, num_tokens, workspace,
@@ -325,6 +379,42 @@ extern "C" int nva_argmax_accept(const void* logits, int64_t row_stride, int32_t
       static_cast<const uint64_t*>(workspace), chunks, num_tokens, cu_seqlens_q, num_seqs,
       input_ids, argmax, accept_len, bonus);
   return launch_status();
+}
+
+}  // namespace
+
+extern "C" int nva_argmax_accept(const void* logits, int64_t row_stride, int32_t vocab,
+                                 const int32_t* cu_seqlens_q, int32_t num_seqs,
+                                 int32_t num_tokens, const int64_t* input_ids, int32_t* argmax,
+                                 int32_t* accept_len, int32_t* bonus, void* workspace,
+                                 size_t workspace_bytes_, void* stream) {
+  const int st = check_accept_args(logits, row_stride, vocab, cu_seqlens_q, num_seqs,
+                                   num_tokens, input_ids, argmax, accept_len, bonus);
+  if (st != NVA_OK || num_seqs == 0) return st;
+  return argmax_accept_launch(logits, row_stride, vocab, cu_seqlens_q, num_seqs, num_tokens,
+                              input_ids, argmax, accept_len, bonus, workspace, workspace_bytes_,
+                              static_cast<hipStream_t>(stream));
+}
+
+extern "C" int nva_argmax_accept_static(const void* logits, int64_t row_stride, int32_t vocab,
+                                        const int32_t* cu_seqlens_q, int32_t num_seqs,
+                                        int32_t num_tokens, const int64_t* input_ids,
+                                        int32_t* argmax, int32_t* accept_len, int32_t* bonus,
+                                        void* stream) {
+  int st = check_accept_args(logits, row_stride, vocab, cu_seqlens_q, num_seqs, num_tokens,
+                             input_ids, argmax, accept_len, bonus);
+  if (st != NVA_OK || num_seqs == 0) return st;
+  if (static_cast<int64_t>(num_tokens) * row_chunks(vocab) > NVA_ARGMAX_STATIC_KEYS)
+    return NVA_ERR_CAPACITY;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  void* ws = nullptr;
+  st = static_scratch(s, &ws);
+  if (st != NVA_OK) return st;
+  // every chunk key the merge reads is written by this call's first launch,
+  // so the array needs no clearing between calls
+  return argmax_accept_launch(logits, row_stride, vocab, cu_seqlens_q, num_seqs, num_tokens,
+                              input_ids, argmax, accept_len, bonus, ws,
+                              sizeof(uint64_t) * (NVA_ARGMAX_STATIC_KEYS + 2), s);
 }
 
 extern "C" int nva_argmax_rows(const void* logits, int64_t row_stride, int32_t vocab,

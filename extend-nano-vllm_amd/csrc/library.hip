@@ -8,6 +8,7 @@ extern "C" const char* nva_status_string(int status) {
     case NVA_ERR_WORKSPACE: return "workspace missing or too small";
     case NVA_ERR_UNSUPPORTED: return "unsupported configuration";
     case NVA_ERR_LAUNCH: return "kernel launch failed";
+    case NVA_ERR_CAPACITY: return "input exceeds the static scratch capacity";
     default: return "unknown status";
   }
 }

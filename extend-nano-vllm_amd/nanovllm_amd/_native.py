@@ -19,6 +19,8 @@ NVA_ERR_ARG = 1
 NVA_ERR_WORKSPACE = 2
 NVA_ERR_UNSUPPORTED = 3
 NVA_ERR_LAUNCH = 4
+NVA_ERR_CAPACITY = 5
+ARGMAX_STATIC_KEYS = 65536      # NVA_ARGMAX_STATIC_KEYS of the header
 
 KV_BF16 = 0
 KV_FP8_E4M3 = 1
@@ -42,6 +44,7 @@ SIGNATURES = {
     "nva_aux_gather": (_INT, [_P, _P, _I32, _I64, _I32, _I32, _P, _I32, _P, _I64, _P]),
     "nva_argmax_workspace_size": (_SZ, [_I32, _I32, _I32]),
     "nva_argmax_accept": (_INT, [_P, _I64, _I32, _P, _I32, _I32, _P, _P, _P, _P, _P, _SZ, _P]),
+    "nva_argmax_accept_static": (_INT, [_P, _I64, _I32, _P, _I32, _I32, _P, _P, _P, _P, _P]),
     "nva_argmax_rows": (_INT, [_P, _I64, _I32, _I32, _P, _P, _P, _SZ, _P]),
     "nva_paged_attention_workspace_size": (_SZ, [_I32, _I32, _I32, _I32, _I32, _I32, _I32]),
     "nva_paged_attention_varlen": (_INT, [_P, _I64, _I64, _P, _P, _INT, _I64, _I64, _I64, _I32,
@@ -108,6 +111,6 @@ def check(status: int, what: str) -> None:
     if status == NVA_OK:
         return
     msg = load().nva_status_string(status).decode()
-    if status in (NVA_ERR_ARG, NVA_ERR_UNSUPPORTED):
+    if status in (NVA_ERR_ARG, NVA_ERR_UNSUPPORTED, NVA_ERR_CAPACITY):
         raise ValueError(f"{what}: {msg} (status {status})")
     raise KernelError(f"{what}: {msg} (status {status})")

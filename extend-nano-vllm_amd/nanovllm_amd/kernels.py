@@ -277,6 +277,36 @@ def argmax_accept(logits: torch.Tensor, cu_seqlens_q: torch.Tensor, input_ids: t
     return argmax, acc, bonus
 
 
+def argmax_accept_static(logits: torch.Tensor, cu_seqlens_q: torch.Tensor,
+                         input_ids: torch.Tensor, out: torch.Tensor) -> tuple:
+    """``argmax_accept`` through the allocation-free entry point
+    (``nva_argmax_accept_static``): the chunk keys go to the library's static
+    per-device array instead of a workspace, and the caller provides ``out``
+    (int32, at least T + 2B entries), so nothing is allocated on any path.
+    Raises ValueError when T * ceil(V / 16384) exceeds the array
+    (``_native.ARGMAX_STATIC_KEYS`` keys).  Calls that overlap on one GPU
+    share the array and must be serialised."""
+    lib = _native.load()
+    _require_cuda(logits, cu_seqlens_q, input_ids, out)
+    if logits.dtype != BF16 or logits.dim() != 2 or logits.stride(1) != 1:
+        raise ValueError("logits must be bf16 [T, V] with unit last stride")
+    _i32(cu_seqlens_q, "cu_seqlens_q")
+    if input_ids.dtype != torch.int64 or not input_ids.is_contiguous():
+        raise TypeError("input_ids must be contiguous int64")
+    t, v = logits.shape
+    b = cu_seqlens_q.numel() - 1
+    if input_ids.numel() != t:
+        raise ValueError("input_ids must have one entry per logits row")
+    if out.dtype != torch.int32 or not out.is_contiguous() or out.numel() < t + 2 * b:
+        raise ValueError("out must be contiguous int32 with at least T + 2B entries")
+    argmax, acc, bonus = out[:t], out[t:t + b], out[t + b:t + 2 * b]
+    check(lib.nva_argmax_accept_static(logits.data_ptr(), logits.stride(0), v,
+                                       cu_seqlens_q.data_ptr(), b, t, input_ids.data_ptr(),
+                                       argmax.data_ptr(), acc.data_ptr(), bonus.data_ptr(),
+                                       _stream()), "argmax_accept_static")
+    return argmax, acc, bonus
+
+
 def argmax_rows(logits: torch.Tensor, index_map: torch.Tensor | None = None,
                 out: torch.Tensor | None = None) -> torch.Tensor:
     """Greedy token per row: argmax (+ index_map[argmax]) as int64.

@@ -38,7 +38,8 @@ enum nva_status {
   NVA_ERR_ARG = 1,          /* null pointer, bad size/stride/shape */
   NVA_ERR_WORKSPACE = 2,    /* workspace missing or smaller than required */
   NVA_ERR_UNSUPPORTED = 3,  /* valid but unsupported (e.g. head_dim != 128) */
-  NVA_ERR_LAUNCH = 4        /* the HIP runtime rejected a launch */
+  NVA_ERR_LAUNCH = 4,       /* the HIP runtime rejected a launch */
+  NVA_ERR_CAPACITY = 5      /* input larger than a static scratch array holds */
 };
 
 enum nva_kv_dtype { NVA_KV_BF16 = 0, NVA_KV_FP8_E4M3 = 1 };
@@ -159,6 +160,30 @@ int nva_argmax_accept(const void *logits, int64_t row_stride, int32_t vocab,
                       const int64_t *input_ids,
                       int32_t *argmax, int32_t *accept_len, int32_t *bonus,
                       void *workspace, size_t workspace_bytes, void *stream);
+
+/* Allocation-free variant of nva_argmax_accept.  No counterpart in the
+ *   reference: it is for callers that cannot allocate device memory (code
+ *   under HIP graph capture, tight serving loops, harnesses that forbid
+ *   hipMalloc).  Same arguments, outputs and launches as nva_argmax_accept,
+ *   without the workspace: the chunk keys go to a static device array of
+ *   NVA_ARGMAX_STATIC_KEYS 64-bit keys (512 KiB) that each GPU holds until
+ *   the process ends.  Its address is looked up once per device
+ *   (hipGetSymbolAddress) on the first call made with that device current.
+ * Limit: num_tokens * ceil(vocab / 16384) <= NVA_ARGMAX_STATIC_KEYS (6553
+ *   rows of a 151936-token vocabulary); larger inputs return
+ *   NVA_ERR_CAPACITY and launch nothing.  The stream must belong to the
+ *   current device (NVA_ERR_ARG otherwise).
+ * Nothing is allocated, freed or cleared: every key the merge reads is
+ *   written earlier in the same call.  All calls on one GPU share the array,
+ *   so calls that overlap on one GPU (other streams, other host threads) race
+ *   and must be serialised by the caller. */
+#define NVA_ARGMAX_STATIC_KEYS 65536
+
+int nva_argmax_accept_static(const void *logits, int64_t row_stride, int32_t vocab,
+                             const int32_t *cu_seqlens_q, int32_t num_seqs, int32_t num_tokens,
+                             const int64_t *input_ids,
+                             int32_t *argmax, int32_t *accept_len, int32_t *bonus,
+                             void *stream);
 
 /* ---------------------------------------------------------------------
  * K4b  Row argmax with an optional index map (greedy sampling).

@@ -51,6 +51,17 @@ def test_host_side_argument_errors_without_gpu():
                                           None, 0, None) == _native.NVA_ERR_UNSUPPORTED
     assert lib.nva_argmax_accept(None, 10, 5, None, 1, 1, None, None, None, None, None, 0,
                                  None) == _native.NVA_ERR_ARG
+    # the allocation-free argmax refuses more chunk keys than its static
+    # array holds on the host (the pointers are never touched): 6554 rows of
+    # ten 16384-element chunks need 65540 keys; 6553 rows would fit
+    fake = 4096
+    assert _native.ARGMAX_STATIC_KEYS == 65536
+    assert lib.nva_argmax_accept_static(fake, 151936, 151936, fake, 1, 6554, fake, fake, fake,
+                                        fake, None) == _native.NVA_ERR_CAPACITY
+    assert lib.nva_argmax_accept_static(None, 10, 5, None, 1, 1, None, None, None, None,
+                                        None) == _native.NVA_ERR_ARG
+    with pytest.raises(ValueError, match="static scratch capacity"):
+        _native.check(_native.NVA_ERR_CAPACITY, "probe")
     # zero-size work is a no-op
     assert lib.nva_argmax_rows(None, 8, 8, 0, None, None, None, 0, None) == _native.NVA_OK
     assert lib.nva_argmax_workspace_size(384, 64, 151936) > 0
