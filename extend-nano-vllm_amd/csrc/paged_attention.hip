@@ -133,8 +133,13 @@ __device__ __forceinline__ bf16x8_t fp8x8_to_bf16(uint2 w) {
 // of the key range is one load from a selected pointer (cu_k + 1 or
 // seqlens), issued with the others before any value is used, so the
 // geometry costs one memory latency.
+// q_rows_raw (optional) receives the sequence's row count before the
+// max_seqlen_q clip (bounded by num_tokens the same way).  A sequence
+// clipped to its first max_q rows also drops the keys of its clipped rows
+// (L shrinks by the rows cut), so each kept row j still sees keys
+// [0, L - q_raw + j], its unclipped causal window.
 __device__ __forceinline__ void seq_geometry(const AttnParams& p, int seq, int& q_start, int& q_len,
-                                             int& L) {
+                                             int& L, int* q_rows_raw = nullptr) {
   int q0 = seq, q1 = seq + 1, k0 = 0;
   const int k1 = (p.cu_k ? p.cu_k + 1 : p.seqlens)[seq];
   if (p.cu_q) {
@@ -143,11 +148,12 @@ __device__ __forceinline__ void seq_geometry(const AttnParams& p, int seq, int& 
   }
   if (p.cu_k) k0 = p.cu_k[seq];
   q_start = q0;
-  q_len = q1 - q0;
-  q_len = q_len > p.max_q ? p.max_q : q_len;
-  if (q_start < 0 || q_start >= p.num_tokens) q_len = 0;
-  else if (q_len > p.num_tokens - q_start) q_len = p.num_tokens - q_start;
-  L = k1 - k0;
+  int raw = q1 - q0;
+  if (q_start < 0 || q_start >= p.num_tokens) raw = 0;
+  else if (raw > p.num_tokens - q_start) raw = p.num_tokens - q_start;
+  q_len = raw > p.max_q ? p.max_q : raw;
+  if (q_rows_raw) *q_rows_raw = raw;
+  L = k1 - k0 - (raw - q_len);
   L = L > p.max_k ? p.max_k : L;
 }
 
@@ -156,11 +162,13 @@ __device__ __forceinline__ void seq_geometry(const AttnParams& p, int seq, int& 
 // that they stay in scalar registers (a buffer descriptor built from them
 // would otherwise need a waterfall loop per load).
 __device__ __forceinline__ void seq_geometry_uniform(const AttnParams& p, int seq, int& q_start,
-                                                     int& q_len, int& L) {
-  seq_geometry(p, seq, q_start, q_len, L);
+                                                     int& q_len, int& L,
+                                                     int* q_rows_raw = nullptr) {
+  seq_geometry(p, seq, q_start, q_len, L, q_rows_raw);
   q_start = __builtin_amdgcn_readfirstlane(q_start);
   q_len = __builtin_amdgcn_readfirstlane(q_len);
   L = __builtin_amdgcn_readfirstlane(L);
+  if (q_rows_raw) *q_rows_raw = __builtin_amdgcn_readfirstlane(*q_rows_raw);
 }
 
 // Block ids of the split that starts at key kv_begin, one per lane: lane i
@@ -634,6 +642,25 @@ __device__ __forceinline__ void note_rows(const AttnParams& p, int seq, int qt, 
   for (int j = threadIdx.x; j < jn; j += blockDim.x) p.row_nsplit[q_start + j0 + j] = nsplit;
 }
 
+// Rows q_start + q_len .. q_start + q_raw - 1 of a sequence clipped to
+// max_seqlen_q (cu_seqlens_q gave it more rows than the bound the grid was
+// sized for) get zero output and split count 0, so that combine_kernel
+// leaves them alone instead of merging a stale count left in the workspace
+// by an earlier call.  Threads tid, tid + nthreads, ... share the stores.
+__device__ void clear_clipped_rows(const AttnParams& p, int q_start, int q_len, int q_raw, int tid,
+                                   int nthreads) {
+  const int per_row = p.hq * (kD / 8);
+  for (int t = q_start + q_len; t < q_start + q_raw; ++t) {
+    uint16_t* row = p.out + static_cast<int64_t>(t) * p.out_row_stride;
+    for (int i = tid; i < per_row; i += nthreads) {
+      const int h = i / (kD / 8), c = i % (kD / 8);
+      *reinterpret_cast<uint4*>(row + static_cast<int64_t>(h) * p.out_head_stride + c * 8) =
+          make_uint4(0, 0, 0, 0);
+    }
+    if (p.row_nsplit && tid == 0) p.row_nsplit[t] = 0;
+  }
+}
+
 // keys the single query tile of a sequence sees, in 32-key chunks (stream mode)
 __device__ __forceinline__ int stream_chunks(const AttnParams& p, int seq) {
   int q_start, q_len, L;
@@ -660,13 +687,15 @@ paged_attention_kernel(AttnParams p) {
   const int qt = blockIdx.z / p.max_splits;
   const int kv_begin = split * p.split_len;
   const int lane_blk = split_block_ids(p, seq, kv_begin);
-  int q_start, q_len, L;
-  seq_geometry_uniform(p, seq, q_start, q_len, L);
+  int q_start, q_len, L, q_raw;
+  seq_geometry_uniform(p, seq, q_start, q_len, L, &q_raw);
   const int j0 = qt * p.qtile;
   const int jn = (q_len - j0 < p.qtile) ? q_len - j0 : p.qtile;
   const int kv_limit = L - q_len + j0 + jn;  // meaningful when jn > 0
   const int nsplit = kv_limit > 0 ? (kv_limit + p.split_len - 1) / p.split_len : 0;
   const bool note = kvh == 0 && split == 0 && p.row_nsplit;
+  // rows past max_seqlen_q, if any, are cleared by one workgroup
+  const bool clip_owner = kvh == 0 && split == 0 && qt == p.n_qtiles - 1 && q_raw > q_len;
   // one branch on the whole geometry, so every geometry load is issued
   // before the first wait
   if (jn <= 0 || kv_begin >= kv_limit) {
@@ -674,12 +703,14 @@ paged_attention_kernel(AttnParams p) {
       if (note) note_rows(p, seq, qt, nsplit);
       if (kv_limit <= 0 && split == 0) zero_tile(p, kvh, seq, qt);
     }
+    if (clip_owner) clear_clipped_rows(p, q_start, q_len, q_raw, threadIdx.x, blockDim.x);
     return;
   }
   if (note) note_rows(p, seq, qt, nsplit);
   const int kv_end = kv_begin + p.split_len < kv_limit ? kv_begin + p.split_len : kv_limit;
   attend_segment<NT, FP8, PIPE, WPS>(p, vst, qst, kvh, seq, qt, q_start, q_len, L, kv_begin, kv_end,
                                      split, nsplit, lane_blk);
+  if (clip_owner) clear_clipped_rows(p, q_start, q_len, q_raw, threadIdx.x, blockDim.x);
 }
 
 // Balanced ("stream") decomposition for one query tile per sequence (verify
@@ -730,9 +761,11 @@ paged_attention_stream_kernel(AttnParams p) {
       for (int s = lane; s < p.num_seqs; s += kWave) {
         const int hi = pre[s + 1], lo = pre[s];
         const int ns = hi > lo ? (hi - 1) / rc - lo / rc + 1 : 0;
-        int q_start, q_len, L;
-        seq_geometry(p, s, q_start, q_len, L);
+        int q_start, q_len, L, q_raw;
+        seq_geometry(p, s, q_start, q_len, L, &q_raw);
         for (int j = 0; j < q_len; ++j) p.row_nsplit[q_start + j] = ns;
+        // rows past max_seqlen_q: this lane alone clears them
+        if (q_raw > q_len) clear_clipped_rows(p, q_start, q_len, q_raw, 0, 1);
       }
     }
     // sequences with no visible key get zero rows

@@ -347,6 +347,31 @@ def _cache_args(k_cache: torch.Tensor, v_cache: torch.Tensor):
             hkv, d)
 
 
+def _device_lengths(t, device: torch.device, name: str):
+    """(device int32 tensor, host lengths or None) for a cu_seqlens / seqlens
+    argument.  A device tensor passes through (its values are not read: that
+    would need a synchronisation); a CPU tensor or a list is host-known, so
+    its values are returned for the bound checks and it is copied to the
+    device (not allowed under graph capture)."""
+    if isinstance(t, torch.Tensor) and t.is_cuda:
+        if t.device != device:
+            raise ValueError("all tensors must be on the same device")
+        return t, None
+    host = torch.as_tensor(t, dtype=torch.int32)
+    if host.dim() != 1:
+        raise ValueError(f"{name} must be one-dimensional")
+    if torch.cuda.is_current_stream_capturing():
+        raise RuntimeError(f"{name} on the host cannot be uploaded under graph capture")
+    return host.contiguous().to(device), host.tolist()
+
+
+def _check_bound(bound: int, lengths, what: str, name: str) -> None:
+    longest = max(lengths, default=0)
+    if longest > bound:
+        raise ValueError(f"{name}={bound} is below the longest {what} ({longest}); the kernel "
+                         f"would clip it")
+
+
 def _q_out(q: torch.Tensor, out: torch.Tensor | None):
     if q.dtype != BF16 or q.dim() != 3 or q.stride(-1) != 1:
         raise ValueError("q must be bf16 [tokens, num_heads, head_dim] with unit last stride")
@@ -369,11 +394,25 @@ def paged_attention_varlen(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     Mirrors the reference call flash_attn_varlen_func(q, k_cache, v_cache,
     max_seqlen_q, cu_seqlens_q, max_seqlen_k, cu_seqlens_k, softmax_scale,
     causal=True, block_table) of layers/attention.py:385-395: bottom-right
-    aligned causal mask, GQA by head groups, keys read through block_table."""
+    aligned causal mask, GQA by head groups, keys read through block_table.
+
+    ``max_seqlen_q`` / ``max_seqlen_k`` size the launch; the kernel clips a
+    longer sequence to them (rows past max_seqlen_q come back as zeros, keys
+    past max_seqlen_k are not seen).  When cu_seqlens_q / cu_seqlens_k are
+    given on the host (CPU tensors or lists) their lengths are known here and
+    a bound below them raises ValueError; device tensors are not read."""
     if not causal:
         raise ValueError("only causal paged attention is supported")
     lib = _native.load()
-    _require_cuda(q, k_cache, v_cache, cu_seqlens_q, cu_seqlens_k, block_table, out)
+    _require_cuda(q, k_cache, v_cache, block_table, out)
+    cu_seqlens_q, host_q = _device_lengths(cu_seqlens_q, q.device, "cu_seqlens_q")
+    cu_seqlens_k, host_k = _device_lengths(cu_seqlens_k, q.device, "cu_seqlens_k")
+    if host_q is not None:
+        _check_bound(int(max_seqlen_q), [b - a for a, b in zip(host_q, host_q[1:])],
+                     "query length", "max_seqlen_q")
+    if host_k is not None:
+        _check_bound(int(max_seqlen_k), [b - a for a, b in zip(host_k, host_k[1:])],
+                     "key length", "max_seqlen_k")
     kvd, bstr, tstr, hstr, nb, bs, hkv, d = _cache_args(k_cache, v_cache)
     t, hq, dq = q.shape
     if dq != d:
@@ -412,9 +451,12 @@ def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
     Mirrors flash_attn_with_kvcache(q[:, None], k_cache, v_cache,
     cache_seqlens, block_table, softmax_scale, causal=True) of
     layers/attention.py:396-399.  q: [B, Hq, D].  ``max_seqlen_k`` bounds the
-    lengths (default: every cache slot of one table row)."""
+    lengths (default: every cache slot of one table row); the kernel clips a
+    longer length to it.  When ``cache_seqlens`` is given on the host (a CPU
+    tensor or a list) a bound below its largest value raises ValueError."""
     lib = _native.load()
-    _require_cuda(q, k_cache, v_cache, cache_seqlens, block_table, out)
+    _require_cuda(q, k_cache, v_cache, block_table, out)
+    cache_seqlens, host_lens = _device_lengths(cache_seqlens, q.device, "cache_seqlens")
     kvd, bstr, tstr, hstr, nb, bs, hkv, d = _cache_args(k_cache, v_cache)
     b, hq, dq = q.shape
     if dq != d:
@@ -428,6 +470,8 @@ def paged_attention_decode(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torc
         raise ValueError("cache_seqlens / block_table must have one row per query")
     if max_seqlen_k is None:
         max_seqlen_k = block_table.shape[1] * bs
+    if host_lens is not None:
+        _check_bound(int(max_seqlen_k), host_lens, "context length", "max_seqlen_k")
     out = _q_out(q, out)
     nbytes = attention_workspace_bytes(b, b, hq, hkv, d, 1, max_seqlen_k)
     ws = _WS.get(q.device, "attention", nbytes) if nbytes else None

@@ -232,7 +232,14 @@ int nva_argmax_rows(const void *logits, int64_t row_stride, int32_t vocab, int32
  *   cu_seqlens_q[i] query rows and L_i = cu_seqlens_k[i+1] - cu_seqlens_k[i]
  *   keys including its new rows; causality is bottom-right aligned: query row
  *   j sees keys [0, L_i - q_i + j].  max_seqlen_q / max_seqlen_k bound q_i and
- *   L_i (they size the grid; larger device values are clipped to them). */
+ *   L_i: they size the grid, and the lengths live on the device, where the
+ *   host cannot check them.  A longer sequence is clipped, not refused:
+ *   rows past max_seqlen_q are written as zeros, while the kept rows j <
+ *   max_seqlen_q still see exactly keys [0, L_i - q_i + j]; and when the keys
+ *   those rows see run past max_seqlen_k, only the first max_seqlen_k keys
+ *   are attended (row j's range then ends at max_seqlen_k - q' + j, q' the
+ *   kept rows).  Pass the true maxima (the reference's prepare_prefill does,
+ *   model_runner.py:776-781) or safe upper bounds. */
 size_t nva_paged_attention_workspace_size(int32_t num_seqs, int32_t num_tokens,
                                           int32_t num_q_heads, int32_t num_kv_heads,
                                           int32_t head_dim, int32_t max_seqlen_q,

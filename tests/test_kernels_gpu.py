@@ -346,6 +346,8 @@ def _run_verify(K, cuda, case, fp8=False, head_major=False):
     ("config2", dict(seed=1, batch=32, q_len=5, ctx_lo=512, ctx_hi=4096, hq=16, hkv=8)),
     ("gqa4_k5", dict(seed=2, batch=6, q_len=6, ctx_lo=20, ctx_hi=1500, hq=32, hkv=8)),
     ("gqa8_k7", dict(seed=3, batch=4, q_len=8, ctx_lo=8, ctx_hi=900, hq=64, hkv=8)),
+    # 64-row tiles over 3500-8000 keys: several splits per tile plus the combine
+    ("gqa8_k7_long", dict(seed=16, batch=6, q_len=8, ctx_lo=3500, ctx_hi=8000, hq=64, hkv=8)),
     ("ragged", dict(seed=4, batch=7, q_len=[1, 3, 6, 2, 5, 4, 1], ctx_lo=1, ctx_hi=700, hq=16,
                     hkv=4)),
     ("short", dict(seed=5, batch=5, q_len=3, ctx_lo=3, ctx_hi=40, hq=8, hkv=8)),
@@ -757,3 +759,154 @@ def test_full_size_verify_constant_values(K, cuda, name):
     want = cvec.float().repeat_interleave(group, dim=0)          # [Hq, D]
     err = (out.float() - want[None]).abs().max().item()
     assert err <= 1e-2 * want.abs().max().item() + 1e-6, (name, err)
+
+
+def _sample_rows(c, picks):
+    """Host copies of the pages, query rows and output rows of the sampled
+    sequences of a device_paged_case, re-addressed through a compact block
+    table (sequence n's blocks become ids off_n .. off_n + blocks - 1)."""
+    pages, bt, lens, q_len = c["pages"], c["block_tables"], c["lens"], c["q_len"]
+    bs = pages.shape[3]
+    ks, vs, tables, off = [], [], [], 0
+    for i in picks:
+        n = -(-lens[i] // bs)
+        pg = pages[bt[i, :n].long()].cpu()                # [n, Hkv, 2, bs, D]
+        ks.append(pg[:, :, 0].permute(0, 2, 1, 3))        # [n, bs, Hkv, D]
+        vs.append(pg[:, :, 1].permute(0, 2, 1, 3))
+        tables.append(list(range(off, off + n)))
+        off += n
+    width = max(len(t) for t in tables)
+    sub_bt = np.full((len(picks), width), -1, np.int32)
+    for r, t in enumerate(tables):
+        sub_bt[r, :len(t)] = t
+    rows = torch.tensor([i * q_len + j for i in picks for j in range(q_len)])
+    q = c["q"].index_select(0, rows.to(c["q"].device)).cpu()
+    return (bits(torch.cat(ks).contiguous()), bits(torch.cat(vs).contiguous()), sub_bt, rows,
+            bits(q), np.array([lens[i] for i in picks], np.int32))
+
+
+def _picks(c, count, seed):
+    """The longest and the shortest sequence plus seeded random others."""
+    lens = np.array(c["lens"])
+    rng = np.random.default_rng(seed)
+    picks = {int(lens.argmax()), int(lens.argmin())}
+    while len(picks) < count:
+        picks.add(int(rng.integers(len(lens))))
+    return sorted(picks)
+
+
+@pytest.mark.parametrize("name", list(FULL_CASES))
+def test_full_size_verify_matches_oracle_on_sampled_sequences(K, cuda, name):
+    """At the BASELINE configs' full sizes the whole batch runs on the GPU in
+    one launch (config 4: FP8 pages, stream ranges over 128 sequences of
+    4096-16384 keys; config 5: 64-row tiles, 3072-key splits and the
+    combine, the first 30% of every sequence's blocks shared), and the
+    rows of 8 sampled sequences -- the longest and the shortest among them
+    -- are held to the CPU oracle on the same pages: the textbook attention
+    within 2e-2 (the north star's bound) and, for FP8, the restated
+    reference FP8 decode kernel (attention.py:85-182) within 2e-3 with each
+    verify row expanded into a decode row of context L_i - q_i + j + 1."""
+    from helpers import device_paged_case
+
+    case = FULL_CASES[name]
+    c = device_paged_case(cuda, **case)
+    fp8 = case.get("fp8", False)
+    one = torch.ones(1, device=cuda) if fp8 else None
+    out = K.paged_attention_varlen(c["q"], c["k_cache"], c["v_cache"], c["cu_q"], c["cu_k"],
+                                   c["q_len"], c["max_k"], 128 ** -0.5, c["block_tables"],
+                                   k_scale=one, v_scale=one)
+    torch.cuda.synchronize()
+    picks = _picks(c, 8, seed=5)
+    if not fp8:
+        # config 5: at least one sampled sequence needs three splits
+        assert max(c["lens"][i] for i in picks) > 2 * 3072
+    kb, vb, sub_bt, rows, qb, lens = _sample_rows(c, picks)
+    q_len = c["q_len"]
+    cu = np.arange(0, len(picks) * q_len + 1, q_len, dtype=np.int32)
+    got = out.index_select(0, rows.to(cuda)).float().cpu().numpy()
+    ref = oracle.paged_attention(qb, kb, vb, cu, lens, sub_bt, 128 ** -0.5)
+    err = np.abs(got - ref).max()
+    assert err <= ATTN_TOL, (name, err, picks)
+    if fp8:
+        ctx = np.array([L - q_len + j + 1 for L in lens for j in range(q_len)], np.int32)
+        dec = oracle.fp8_paged_decode(qb, kb, vb, ctx, np.repeat(sub_bt, q_len, axis=0),
+                                      128 ** -0.5)
+        err_dec = np.abs(got - dec).max()
+        assert err_dec <= FP8_TOL, (name, err_dec, picks)
+
+
+@pytest.mark.parametrize("name,kw,clip_to", [
+    # fixed decomposition, 40-row tiles (NT 4) with splits and the combine
+    ("gqa8_fixed", dict(seed=12, batch=6, q_len=[8, 3, 8, 5, 8, 1], ctx_lo=3500, ctx_hi=8000,
+                        hq=64, hkv=8), 5),
+    # fixed decomposition, eight waves per split (16-row tiles)
+    ("gqa4_shared", dict(seed=13, batch=5, q_len=[6, 6, 2, 6, 4], ctx_lo=300, ctx_hi=5000,
+                         hq=32, hkv=8), 4),
+    # FP8 stream decomposition
+    ("fp8_stream", dict(seed=14, batch=6, q_len=[5, 2, 5, 5, 3, 5], ctx_lo=300, ctx_hi=5000,
+                        hq=16, hkv=8, fp8=True), 3),
+])
+def test_rows_past_max_seqlen_q_are_cleared(K, cuda, name, kw, clip_to):
+    """A max_seqlen_q below a sequence's query count clips it: its rows past
+    the bound come back as zeros, its kept rows keep their exact causal
+    windows, and the combine does not merge the stale split counts an
+    earlier call left in the shared workspace for those rows (the first
+    call below runs the same batch unclipped and leaves counts > 1)."""
+    kw = dict(kw)
+    fp8 = kw.pop("fp8", False)
+    case = paged_case(**kw)
+    kc, vc = case["k_cache"], case["v_cache"]
+    if fp8:
+        kc, vc = kc.float().to(torch.float8_e4m3fn), vc.float().to(torch.float8_e4m3fn)
+    dkc, dvc = kc.to(cuda), vc.to(cuda)
+    one = torch.ones(1, device=cuda) if fp8 else None
+    args = (dkc, dvc, case["cu_q"].to(cuda), case["cu_k"].to(cuda))
+    q = case["q"].to(cuda)
+    max_k = int(case["lens"].max())
+    full = K.paged_attention_varlen(q, *args, max(case["q_lens"]), max_k, 128 ** -0.5,
+                                    case["block_tables"].to(cuda), k_scale=one, v_scale=one)
+    out = torch.full_like(q, 7.0)
+    K.paged_attention_varlen(q, *args, clip_to, max_k, 128 ** -0.5, case["block_tables"].to(cuda),
+                             k_scale=one, v_scale=one, out=out)
+    torch.cuda.synchronize()
+    got, full = out.float().cpu(), full.float().cpu()
+    cu = case["cu_q"].tolist()
+    kept_rows, kept_q, kept_lens = [], [], []
+    for i, (qn, L) in enumerate(zip(case["q_lens"], case["lens"].tolist())):
+        keep = min(qn, clip_to)
+        kept_rows += range(cu[i], cu[i] + keep)
+        kept_q.append(keep)
+        kept_lens.append(L - (qn - keep))
+        assert bool((got[cu[i] + keep:cu[i + 1]] == 0).all()), (name, i)
+    kept = torch.tensor(kept_rows)
+    # kept rows: the same values as the unclipped call (to the last bit is
+    # not promised: the split decomposition follows max_seqlen_q) ...
+    assert (got[kept] - full[kept]).abs().max().item() <= 2e-3, name
+    # ... and the oracle of the kept rows with their unclipped windows
+    ref = oracle.paged_attention(bits(case["q"][kept]), bits(kc), bits(vc),
+                                 np.array([0] + np.cumsum(kept_q).tolist(), np.int32),
+                                 np.array(kept_lens, np.int32), case["block_tables"].numpy(),
+                                 128 ** -0.5)
+    assert np.abs(got[kept].numpy() - ref).max() <= ATTN_TOL, name
+
+
+def test_wrappers_refuse_bounds_below_host_lengths(K, cuda):
+    """Host-known lengths (CPU tensors or lists) let the wrappers refuse a
+    max_seqlen below them before any launch; with a sufficient bound the
+    host arguments give the same result as device tensors."""
+    case = paged_case(seed=15, batch=4, q_len=[3, 5, 2, 5], ctx_lo=50, ctx_hi=900, hq=16, hkv=8)
+    kc, vc = case["k_cache"].to(cuda), case["v_cache"].to(cuda)
+    q, bt = case["q"].to(cuda), case["block_tables"].to(cuda)
+    max_k = int(case["lens"].max())
+    with pytest.raises(ValueError, match="max_seqlen_q=4"):
+        K.paged_attention_varlen(q, kc, vc, case["cu_q"], case["cu_k"], 4, max_k, 0.1, bt)
+    with pytest.raises(ValueError, match="max_seqlen_k"):
+        K.paged_attention_varlen(q, kc, vc, case["cu_q"].tolist(), case["cu_k"], 5, max_k - 1,
+                                 0.1, bt)
+    with pytest.raises(ValueError, match="max_seqlen_k"):
+        K.paged_attention_decode(q[:4], kc, vc, case["lens"], bt, 0.1, max_seqlen_k=max_k - 1)
+    host = K.paged_attention_varlen(q, kc, vc, case["cu_q"], case["cu_k"], 5, max_k, 0.1, bt)
+    dev = K.paged_attention_varlen(q, kc, vc, case["cu_q"].to(cuda), case["cu_k"].to(cuda), 5,
+                                   max_k, 0.1, bt)
+    torch.cuda.synchronize()
+    assert torch.equal(host.view(torch.int16), dev.view(torch.int16))
