@@ -342,3 +342,135 @@ def test_verify_metadata_agrees_with_engine_host_path(monkeypatch):
         assert ocu_k.tolist() == ctx.cu_seqlens_k.tolist()
     finally:
         reset_context()
+
+
+# ---------------------------------------------------------------- EAGLE3 draft step
+
+def _draft_weights(seed=0, h=256, hq=4, hkv=2, d=128, inter=512, vocab=300, nbr=True):
+    from oracle.draft_oracle import DraftWeights
+
+    g = torch.Generator().manual_seed(seed)
+    r = lambda *s, std=0.05: torch.randn(*s, generator=g) * std  # noqa: E731
+    n1 = lambda: 1 + r(h, std=0.1)  # noqa: E731
+    return DraftWeights(embed=r(vocab, h, std=1.0), fc=r(h, 3 * h), hidden_norm=n1(),
+                        input_norm=n1(), qkv=r((hq + 2 * hkv) * d, 2 * h), o=r(h, hq * d),
+                        post_norm=n1(), gate_up=r(2 * inter, h), down=r(h, inter), norm=n1(),
+                        lm_head=r(vocab, h), d2t=torch.zeros(vocab, dtype=torch.int64),
+                        num_heads=hq, num_kv_heads=hkv, head_dim=d, eps=1e-6, rope_theta=1e6,
+                        norm_before_residual=nbr)
+
+
+def _llama_config(w):
+    from transformers import LlamaConfig
+
+    h = w.embed.shape[1]
+    return LlamaConfig(hidden_size=h, intermediate_size=w.down.shape[1],
+                       num_attention_heads=w.num_heads, num_key_value_heads=w.num_kv_heads,
+                       head_dim=w.head_dim, rope_theta=w.rope_theta, rms_norm_eps=w.eps,
+                       max_position_embeddings=8192)
+
+
+def test_draft_oracle_norm_rope_mlp_match_transformers_llama():
+    """The restatement's RMSNorm, neox RoPE and gated MLP against the
+    transformers Llama modules (float32): an independent implementation of
+    the same published layer (the EAGLE3 draft layer is Llama-style)."""
+    from transformers.models.llama.modeling_llama import (LlamaMLP, LlamaRMSNorm,
+                                                          LlamaRotaryEmbedding,
+                                                          apply_rotary_pos_emb)
+
+    from oracle import draft_oracle as D
+
+    w = _draft_weights()
+    cfg = _llama_config(w)
+    g = torch.Generator().manual_seed(1)
+    x = torch.randn(7, 256, generator=g) * 3
+    ln = LlamaRMSNorm(256, eps=1e-6)
+    ln.weight.data.copy_(w.hidden_norm)
+    torch.testing.assert_close(D.rms_norm(x, w.hidden_norm, 1e-6), ln(x), rtol=1e-6, atol=1e-6)
+    rot = LlamaRotaryEmbedding(cfg)
+    q = torch.randn(4, 128, generator=g)
+    for pos in (0, 1, 37, 4095):
+        cos, sin = rot(q[None], torch.tensor([[pos]]))
+        ref, _ = apply_rotary_pos_emb(q[None, :, None, :], q[None, :, None, :], cos, sin)
+        torch.testing.assert_close(D.rope(q, pos, w.rope_theta), ref[0, :, 0], rtol=1e-5,
+                                   atol=2e-5)
+    m = LlamaMLP(cfg)
+    m.gate_proj.weight.data.copy_(w.gate_up[:512])
+    m.up_proj.weight.data.copy_(w.gate_up[512:])
+    m.down_proj.weight.data.copy_(w.down)
+    with torch.no_grad():
+        torch.testing.assert_close(D.mlp(w, x[0]), m(x[:1])[0], rtol=1e-5, atol=1e-6)
+
+
+def test_draft_oracle_attention_matches_sdpa_and_closed_forms():
+    """attend() equals torch's scaled_dot_product_attention over the same
+    keys with GQA; a single visible key returns its V row; equal scores
+    return the mean of the V rows."""
+    import torch.nn.functional as F
+
+    from oracle import draft_oracle as D
+
+    g = torch.Generator().manual_seed(2)
+    q = torch.randn(8, 128, generator=g)
+    k = torch.randn(50, 2, 128, generator=g)
+    v = torch.randn(50, 2, 128, generator=g)
+    kk = k.repeat_interleave(4, 1).permute(1, 0, 2)[None]       # [1, Hq, n, D]
+    vv = v.repeat_interleave(4, 1).permute(1, 0, 2)[None]
+    ref = F.scaled_dot_product_attention(q[None, :, None, :], kk, vv)[0, :, 0]
+    torch.testing.assert_close(D.attend(q, k, v), ref, rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(D.attend(q, k[:1], v[:1]), v[0].repeat_interleave(4, 0))
+    flat = torch.zeros(8, 128)
+    torch.testing.assert_close(D.attend(flat, k, v), v.mean(0).repeat_interleave(4, 0))
+
+
+@pytest.mark.parametrize("nbr", [True, False])
+def test_draft_oracle_layer_and_recurrence_closed_forms(nbr):
+    """With zero attention and MLP output projections the draft layer passes
+    its residual through: the pre-norm state is hidden_norm(h) when the norm
+    comes before the residual (eagle3.py:133-135), h itself otherwise, and
+    the sampled state is its final norm.  Then every proposal after the
+    first is the same token (the fed-back state is a fixed point of the
+    normalisation), and a commit's state depends on fc of the last aux row
+    only."""
+    from oracle import draft_oracle as D
+
+    w = _draft_weights(nbr=nbr)
+    w.o.zero_()
+    w.down.zero_()
+    g = torch.Generator().manual_seed(3)
+    h = torch.randn(256, generator=g)
+    hist = torch.randn(5, 2, 128, generator=g)
+    normed, pre, k, v = D.forward_token(w, 17, 5, h, hist, hist)
+    want_pre = D.rms_norm(h, w.hidden_norm, w.eps) if nbr else h
+    torch.testing.assert_close(pre, want_pre)
+    torch.testing.assert_close(normed, D.rms_norm(want_pre, w.norm, w.eps))
+    # the new V row is the value projection of [norm(embed) | norm(h)]
+    attn_in = torch.cat((D.rms_norm(w.embed[17], w.input_norm, w.eps),
+                         D.rms_norm(h, w.hidden_norm, w.eps)))
+    torch.testing.assert_close(v, (w.qkv[(4 + 2) * 128:] @ attn_in).view(2, 128))
+    if nbr:
+        w.hidden_norm.fill_(1.0)
+        toks, rows, ks, vs = D.propose(w, D.rms_norm(h, w.norm, w.eps), h, 5, 4, hist, hist)
+        assert len(set(toks[1:])) == 1 and ks.shape == (3, 2, 128)
+        fixed = D.rms_norm(D.rms_norm(h, w.hidden_norm, w.eps), w.norm, w.eps)
+        assert toks[1] == int(torch.argmax(w.lm_head @ fixed))
+    aux = torch.randn(3, 768, generator=g)
+    n1, p1, ks, _ = D.commit(w, [3, 9, 11], aux, 5, hist, hist)
+    n2, p2, _, _ = D.commit(w, [40, 9, 11], torch.cat((torch.randn(2, 768, generator=g),
+                                                       aux[2:])), 5, hist, hist)
+    torch.testing.assert_close(p1, p2)
+    assert ks.shape == (3, 2, 128)
+
+
+def test_draft_oracle_sampling_maps_through_d2t():
+    """sample_greedy returns argmax + d2t[argmax] (eagle3.py:294-296)."""
+    from oracle import draft_oracle as D
+
+    w = _draft_weights()
+    w.lm_head.zero_()
+    x = torch.ones(256)
+    w.lm_head[123] = 1.0                      # argmax row 123
+    w.d2t[123] = 1000
+    assert D.sample_greedy(w, x) == 1123
+    w.lm_head[200] = 1.0                      # a tie: the first index wins
+    assert D.sample_greedy(w, x) == 1123
