@@ -73,9 +73,16 @@ def parse_args():
     ap.add_argument("--roofline-repeats", type=int, default=10,
                     help="times the verify-attention launches of one step are re-issued "
                          "between HIP events for the roofline figure")
-    ap.add_argument("--reference-steps", type=int, default=3,
-                    help="steps timed with the reference's step structure for comparison "
-                         "(0 to skip)")
+    ap.add_argument("--reference-steps", type=int, default=5,
+                    help="steps timed with the reference's step structure for comparison, on "
+                         "this build's kernels and on torch attention (0 to skip)")
+    ap.add_argument("--acceptance-steps", type=int, default=20,
+                    help="steps of the forced-acceptance run (0 to skip)")
+    ap.add_argument("--draft-keep", type=float, default=0.7,
+                    help="forced-acceptance run: probability that a draft position carries "
+                         "the target's greedy token")
+    ap.add_argument("--no-per-config", action="store_true",
+                    help="skip the per-config kernel figures of the JSON line")
     ap.add_argument("--gemm-tuning", default=DEFAULT_GEMM_TUNING,
                     help="TunableOp results for the projection GEMMs ('' for library defaults)")
     ap.add_argument("--kv-layout", default="head_major", choices=["head_major", "token_major"],
@@ -227,8 +234,9 @@ def attention_only(args) -> None:
     in one cache per layer (block ids shuffled), so that consecutive calls
     read different pages as the step's layers do.  Launches
     ``--roofline-repeats`` x 36 verify-attention calls (one step's worth per
-    repeat, layer by layer), then a plain device copy of 1 GiB as often, for
-    scaling FETCH_SIZE / WRITE_SIZE counter readings to bytes."""
+    repeat, layer by layer), then a plain device copy of 1 GiB and a 1 GiB
+    read (a sum) as often, for scaling FETCH_SIZE / WRITE_SIZE counter
+    readings to bytes."""
     import torch
 
     from nanovllm_amd import kernels
@@ -298,6 +306,11 @@ def attention_only(args) -> None:
     n_attn = args.roofline_repeats * layers
     attn_us = timed(attn, n_attn)
     copy_us = timed(lambda: dst.copy_(src), args.roofline_repeats)
+    # a read-only reference (1 GiB read, 4 bytes written): the FETCH_SIZE
+    # scale for a kernel that reads with wide vector loads and writes little
+    total = torch.empty(1, dtype=torch.float32, device=dev)
+    flat = src.view(torch.float32)
+    read_us = timed(lambda: torch.sum(flat, 0, out=total), args.roofline_repeats)
     byts = sum(seqlens) * hkv * d * 2 * 2 + T * hq * d * 2 * 2
     print(json.dumps({"workload": "verify attention only", "batch": args.batch, "q_len": q_len,
                       "kv_layout": args.kv_layout,
@@ -307,15 +320,110 @@ def attention_only(args) -> None:
                       "achieved_GBs": round(byts / attn_us / 1e3, 1),
                       "copy_bytes": src.numel(), "copy_calls": args.roofline_repeats + 3,
                       "copy_us": round(copy_us, 1),
-                      "copy_GBs": round(2 * src.numel() / copy_us / 1e3, 1)}), flush=True)
+                      "copy_GBs": round(2 * src.numel() / copy_us / 1e3, 1),
+                      "read_calls": args.roofline_repeats + 3, "read_us": round(read_us, 1),
+                      "read_GBs": round(src.numel() / read_us / 1e3, 1)}), flush=True)
+
+
+class TorchAttention:
+    """Paged attention in plain torch ops, standing in for FlashAttention-2
+    in the reference-structured comparator (the reference calls
+    flash_attn_varlen_func / flash_attn_with_kvcache, layers/attention.py:
+    385-399; flash-attn is not installed on this box).  Replaces
+    Attention.attend while installed: every sequence's pages are gathered
+    through the block table into one padded [B, Hkv, L, D] tensor, then a
+    bf16 batched QK^T, the bottom-right causal mask and an fp32 softmax,
+    and a bf16 batched PV -- a few launches per layer whatever the batch,
+    as one FA2 call would be.  Both right-hand operands are made contiguous
+    before the batched products (transposed bf16 views there have faulted
+    the GPU on this pool).  The per-forward metadata is read to the host
+    once and shared by all layers (FA2 would read it on the device)."""
+
+    def __init__(self):
+        self.saved = None
+        self.meta_key = None
+        self.meta = None
+
+    def install(self):
+        import nanovllm_amd.layers as layers
+
+        self.saved = layers.Attention.attend
+        backend = self
+
+        def attend(layer, q):
+            return backend.attend(layer, q)
+
+        layers.Attention.attend = attend
+
+    def uninstall(self):
+        import nanovllm_amd.layers as layers
+
+        layers.Attention.attend = self.saved
+        self.meta_key = self.meta = None
+
+    def _host_meta(self, ctx):
+        # the key holds the metadata tensors themselves (compared by
+        # identity), so none is freed and replaced by a new one at the same id
+        key = (ctx.cu_seqlens_q, ctx.cu_seqlens_k, ctx.context_lens, ctx.block_tables)
+        if self.meta_key is None or any(a is not b for a, b in zip(key, self.meta_key)):
+            if ctx.is_prefill:
+                cu_q = ctx.cu_seqlens_q.tolist()
+                cu_k = ctx.cu_seqlens_k.tolist()
+                qn = [b - a for a, b in zip(cu_q, cu_q[1:])]
+                lens = [b - a for a, b in zip(cu_k, cu_k[1:])]
+            else:
+                lens = ctx.context_lens.tolist()
+                qn = [1] * len(lens)
+                cu_q = list(range(len(lens) + 1))
+            self.meta_key, self.meta = key, (cu_q, qn, lens)
+        return self.meta
+
+    def attend(self, layer, q):
+        import torch
+
+        from nanovllm_amd.context import get_context
+
+        ctx = get_context()
+        cu_q, qn, lens = self._host_meta(ctx)
+        kc, vc = layer.k_cache, layer.v_cache                 # [blocks, bs, Hkv, D] views
+        b, bs, hkv, d = len(lens), kc.shape[1], kc.shape[2], kc.shape[3]
+        hq = q.shape[1]
+        g = hq // hkv
+        lmax, qmax = max(lens), max(qn)
+        nblk = -(-lmax // bs)
+        dev = q.device
+        idx = ctx.block_tables[:b, :nblk].long().clamp_min(0)
+        k = kc[idx].reshape(b, nblk * bs, hkv, d)[:, :lmax]   # gather: [B, L, Hkv, D]
+        v = vc[idx].reshape(b, nblk * bs, hkv, d)[:, :lmax]
+        kt = k.permute(0, 2, 3, 1).contiguous()                # [B, Hkv, D, L]
+        vv = v.permute(0, 2, 1, 3).contiguous()                # [B, Hkv, L, D]
+        # query rows padded to [B, qmax]
+        rows = torch.tensor([cu_q[i] + j for i in range(b) for j in range(qmax)], device=dev)
+        valid = torch.tensor([j < qn[i] for i in range(b) for j in range(qmax)], device=dev)
+        qp = q.index_select(0, rows.clamp_max(q.shape[0] - 1)).view(b, qmax, hkv, g, d)
+        qq = qp.permute(0, 2, 3, 1, 4).reshape(b, hkv, g * qmax, d)
+        s = torch.matmul(qq, kt).float().view(b, hkv, g, qmax, lmax) * layer.scale
+        last = (torch.tensor(lens, device=dev) - torch.tensor(qn, device=dev))[:, None] + \
+            torch.arange(qmax, device=dev)[None, :]           # last visible key per row
+        vis = torch.arange(lmax, device=dev)[None, None, :] <= last[:, :, None]
+        s = s.masked_fill(~vis[:, None, None], float("-inf"))
+        p = torch.softmax(s, -1).nan_to_num_(0.0).to(q.dtype).view(b, hkv, g * qmax, lmax)
+        o = torch.matmul(p, vv).view(b, hkv, g, qmax, d).permute(0, 3, 1, 2, 4)
+        o = o.reshape(b * qmax, hq, d)[valid]
+        if o.shape[0] == q.shape[0]:
+            return o
+        out = torch.zeros_like(q)                              # rows past the batch
+        out[:o.shape[0]] = o
+        return out
 
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def kernel_configs(args) -> None:
-    """Each hot-path kernel alone, at the BASELINE configs' shapes.
+def kernel_configs(args, cpu_seconds: float = 0.0) -> list:
+    """Each hot-path kernel alone, at the BASELINE configs' shapes; returns
+    one record per (kernel, config).
 
     Seeds follow the configs' order (config 1: 0 ... config 5: 4).  Inputs
     are device-resident before timing.  ``iters`` launches are captured in a
@@ -327,7 +435,12 @@ def kernel_configs(args) -> None:
                     bytes; its prefix-shared pages are read once per sharer);
       K2 store:     T*Hkv*D*(2 + esz)*2 (read bf16 rows, write cache rows);
       K3 aux:       R*3H*2*2 read + R*3H*2 written;
-      K4 argmax:    rows*V*2 read."""
+      K4 argmax:    rows*V*2 read.
+    With cpu_seconds > 0, the acceptance configs also time the reference's
+    host acceptance logic (oracle.reference_cpu_acceptance) on the same
+    seeded bf16 bytes the kernel reads, with every host core and with one."""
+    import statistics
+
     import torch
 
     from nanovllm_amd import kernels
@@ -356,11 +469,41 @@ def kernel_configs(args) -> None:
         torch.cuda.synchronize()
         return s.elapsed_time(e) / iters * 1e3
 
+    records = []
+
     def emit(kernel, config, us, byts, **extra):
         gbs = byts / us / 1e3
-        print(json.dumps({"bench": "kernels", "kernel": kernel, "config": config,
-                          "us": round(us, 2), "bytes": int(byts), "GBs": round(gbs, 1),
-                          "frac": round(gbs / HBM_PEAK_GBS, 4), **extra}), flush=True)
+        records.append({"kernel": kernel, "config": config, "us": round(us, 2),
+                        "bytes": int(byts), "GBs": round(gbs, 1),
+                        "frac": round(gbs / HBM_PEAK_GBS, 4), **extra})
+        log(f"kernel {kernel} / {config}: {us:.2f} us")
+
+    def cpu_acceptance(lg_cpu, q_len, batch, ids_cpu):
+        """The reference's per-sequence argmax + verify on the host, timed
+        as the median of >= 20 runs after 3 warm-ups, all cores then one."""
+        from oracle import oracle
+
+        cu = list(range(0, batch * q_len + 1, q_len))
+        ids = ids_cpu.tolist()
+        cores = len(os.sched_getaffinity(0))
+        out = {"cores": cores, "kind": "port"}
+        for key, threads in (("all_cores", cores), ("one_thread", 1)):
+            torch.set_num_threads(threads)
+            for _ in range(3):
+                oracle.reference_cpu_acceptance(lg_cpu, cu, ids)
+            times = []
+            t_end = time.perf_counter() + cpu_seconds / 2
+            while len(times) < 20 or time.perf_counter() < t_end:
+                t0 = time.perf_counter()
+                oracle.reference_cpu_acceptance(lg_cpu, cu, ids)
+                times.append(time.perf_counter() - t0)
+                if len(times) >= 2000:
+                    break
+            med = statistics.median(times)
+            out[key] = {"threads": threads, "us_per_batch": round(med * 1e6, 1),
+                        "rows_per_s": round(batch * q_len / med, 1), "runs": len(times)}
+        torch.set_num_threads(cores)
+        return out
 
     def pages(seed, batch, q_len, lo, hi, hq, hkv, fp8=False, shared_frac=0.0, copies=1):
         g = torch.Generator().manual_seed(seed)
@@ -448,7 +591,8 @@ def kernel_configs(args) -> None:
         slots = c["slots"].clone()
         seqlens = torch.tensor(c["lens"], dtype=torch.int32, device=dev)
         us = timed(lambda: kernels.rollback(c["cu_q"], acc, slots, seqlens))
-        emit("K2 rollback (slots only)", name, us, b * 4 * 3 + c["T"] * 4, seqs=b)
+        emit("K2 rollback (slots only)", name, us, b * 4 * 3 + c["T"] * 4, seqs=b,
+             on_step=False)
 
     # config 1: greedy acceptance, [8, 5, V] logits, drafts raised with p = 0.7
     def acceptance(name, seed, batch, k):
@@ -461,12 +605,17 @@ def kernel_configs(args) -> None:
             for j in range(k):
                 if hit[s_, j]:
                     logits[s_, j, prop[s_, j]] = logits[s_, j].max() + 1.0
-        lg = logits.view(batch * q_len, V).to(torch.bfloat16).to(dev)
-        ids = torch.cat([torch.randint(0, V, (batch, 1), generator=g), prop], 1)
-        ids = ids.reshape(-1).to(dev)
+        lg_cpu = logits.view(batch * q_len, V).to(torch.bfloat16)
+        lg = lg_cpu.to(dev)
+        ids_cpu = torch.cat([torch.randint(0, V, (batch, 1), generator=g), prop], 1).reshape(-1)
+        ids = ids_cpu.to(dev)
         cu = torch.arange(0, batch * q_len + 1, q_len, dtype=torch.int32, device=dev)
         us = timed(lambda: kernels.argmax_accept(lg, cu, ids))
-        emit("K4 argmax_accept", name, us, batch * q_len * V * 2, rows=batch * q_len, vocab=V)
+        extra = {}
+        if cpu_seconds > 0:
+            extra["cpu_baseline"] = cpu_acceptance(lg_cpu, q_len, batch, ids_cpu)
+        emit("K4 argmax_accept", name, us, batch * q_len * V * 2, rows=batch * q_len, vocab=V,
+             **extra)
 
     acceptance("config1 B8 k4", 0, 8, 4)
     acceptance("config3 verify rows B64 k5", 2, 64, 5)
@@ -497,6 +646,160 @@ def kernel_configs(args) -> None:
 
     c5 = pages(4, 128, 8, 2048, 8192, 64, 8, shared_frac=0.3)
     attention("config5 B128 q8 Qwen3-32B (30% shared prefix pages)", c5)
+    del c5
+    torch.cuda.empty_cache()
+    return records
+
+
+def make_engine(args, tmp: str):
+    """The bench workload's engine (random weights, seeded)."""
+    from nanovllm_amd import LLM
+    from nanovllm_amd.synthetic import default_aux_layers, write_eagle3_config, write_qwen3_config
+
+    target = write_qwen3_config(os.path.join(tmp, "target"), args.preset)
+    aux = default_aux_layers(args.preset)
+    draft = write_eagle3_config(os.path.join(tmp, "draft"), args.preset, aux_layers=aux)
+    max_len = args.prompt_max + args.max_tokens
+    blocks_per_seq = -(-(max_len + args.k + 1) // 256)
+    return LLM(target, load_format="dummy", seed=0, max_num_seqs=args.batch,
+               max_model_len=max_len, num_kvcache_blocks=args.batch * blocks_per_seq + 8,
+               max_num_batched_tokens=16384, enable_prefill_batching=True,
+               enforce_eager=args.eager, kv_cache_layout=args.kv_layout,
+               gemm_tuning_file=(args.gemm_tuning or None) if args.preset == "qwen3-8b" else None,
+               speculative_config={"method": "eagle3", "model": draft,
+                                   "num_speculative_tokens": args.k,
+                                   "aux_hidden_state_layers": aux})
+
+
+def add_prompts(llm, args):
+    """The seeded prompts (lengths U[prompt_min, prompt_max], random ids);
+    returns the prompt token lists in request order."""
+    import torch
+
+    from nanovllm_amd import SamplingParams
+
+    vocab = llm.config.hf_config.vocab_size
+    g = torch.Generator().manual_seed(args.seed)
+    lens = torch.randint(args.prompt_min, args.prompt_max + 1, (args.batch,), generator=g).tolist()
+    sp = SamplingParams(temperature=0.0, max_tokens=args.max_tokens, ignore_eos=True)
+    prompts = []
+    for L in lens:
+        prompts.append(torch.randint(0, vocab, (L,), generator=g).tolist())
+        llm.add_request(prompts[-1], sp)
+    return prompts
+
+
+def release(llm) -> None:
+    import gc
+
+    import torch
+
+    llm.exit()
+    del llm
+    gc.collect()
+    torch.cuda.empty_cache()
+
+
+def timed_steps(llm, steps: int):
+    """Wall time and committed tokens of ``steps`` engine steps (synchronised
+    on both sides), plus the engine's speculation counters over them."""
+    import torch
+
+    before = dict(llm.spec_stats)
+    committed = 0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        _, num_tokens = llm.step()
+        committed += -num_tokens
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    return elapsed, committed, {k: llm.spec_stats[k] - before[k] for k in before}
+
+
+def reference_steps(llm, steps: int, torch_attention: bool):
+    """The reference's step structure (llm_engine.py:124-178): one warm-up
+    step, then ``steps`` timed ones; on this build's attention kernel or on
+    the torch stand-in for FA2."""
+    backend = TorchAttention() if torch_attention else None
+    if backend:
+        backend.install()
+    llm.reference_pipeline = True
+    try:
+        llm.step()
+        elapsed, committed, _ = timed_steps(llm, steps)
+    finally:
+        llm.reference_pipeline = False
+        if backend:
+            backend.uninstall()
+    return {"value": round(committed / elapsed, 1), "unit": "tok/s",
+            "ms_per_step": round(elapsed / steps * 1e3, 2), "steps": steps,
+            "attention": ("torch paged gather + batched bf16 matmul / fp32 softmax (stand-in for "
+                          "FlashAttention-2, flash_attn_varlen_func / flash_attn_with_kvcache at "
+                          "layers/attention.py:385-399)") if torch_attention else
+                         "this build's K1",
+            "structure": "reference llm_engine.py:124-178 step shape: eager draft loop with a "
+                         "host sync per draft step, eager target verify with one torch argmax + "
+                         ".tolist() per sequence, host acceptance per sequence, serial "
+                         "single-token draft replay per committed token "
+                         "(model_runner.py:1127-1156)"}
+
+
+def forced_acceptance(args, tmp: str, continuations):
+    """The workload with accepted drafts: a fresh engine (same seeded
+    weights and prompts) whose proposals are rewritten on the device, right
+    after the draft graph, to the target's greedy continuation recorded by
+    the main run, each draft position keeping the target's token with
+    probability args.draft_keep (a seeded choice per sequence and position)
+    and otherwise a different id.  The rewrite is one small host-to-device
+    copy and one gather per step inside the timed region."""
+    import torch
+
+    llm = make_engine(args, tmp)
+    runner = llm.model_runner
+    prompts = add_prompts(llm, args)
+    vocab = llm.config.hf_config.vocab_size
+    width = max(len(c) for c in continuations.values()) + args.k + 1
+    rng = torch.Generator().manual_seed(args.seed + 100)
+    table = torch.zeros(len(prompts), width, dtype=torch.int64)
+    for i, p in enumerate(prompts):
+        cont = torch.tensor(continuations[tuple(p)], dtype=torch.int64)
+        keep = torch.rand(cont.numel(), generator=rng) < args.draft_keep
+        table[i, :cont.numel()] = torch.where(keep, cont, (cont + 1) % vocab)
+    table = table.to(runner.device)
+    row_of = {seq.seq_id: i for i, seq in enumerate(llm.scheduler.waiting)}
+    pinned = torch.empty(2 * args.batch, dtype=torch.int64, pin_memory=True)
+
+    def override(seqs, tokens):
+        b, k = len(seqs), tokens.shape[0]
+        pinned[:b] = torch.tensor([row_of[s.seq_id] for s in seqs])
+        pinned[b:2 * b] = torch.tensor([len(s) for s in seqs])
+        info = pinned[:2 * b].to(tokens.device, non_blocking=True)
+        pos = info[b:][None, :] + torch.arange(k, device=tokens.device)[:, None]
+        tokens[:, :b] = table[info[:b][None, :].expand(k, b), pos]
+
+    try:
+        while llm.scheduler.waiting:
+            llm.step()
+        runner.draft_override = override
+        for _ in range(3):
+            llm.step()
+        n_active = len(llm.scheduler.running)
+        elapsed, committed, stats = timed_steps(llm, args.acceptance_steps)
+    finally:
+        runner.draft_override = None
+        release(llm)
+    seq_steps = max(stats["steps"] * n_active, 1)
+    return {"value": round(committed / elapsed, 1), "unit": "tok/s",
+            "ms_per_step": round(elapsed / args.acceptance_steps * 1e3, 3),
+            "steps": args.acceptance_steps, "warmup": 3, "active_seqs": n_active,
+            "draft_keep": args.draft_keep,
+            "accepted_drafts_per_seq_step": round(stats["accepted"] / seq_steps, 4),
+            "mean_acceptance_length": round(stats["committed"] / seq_steps, 4),
+            "position_accept_rate": round(stats["accepted"] / max(stats["drafted"], 1), 4),
+            "drafts": "target-greedy continuation of each sequence (recorded by the main run, "
+                      "whose steps commit exactly the target's argmax), kept per position with "
+                      "probability draft_keep"}
 
 
 def main():
@@ -509,39 +812,21 @@ def main():
         attention_only(args)
         return
     if args.kernels:
-        kernel_configs(args)
+        for rec in kernel_configs(args, 0.0 if args.no_cpu_baseline else 4.0):
+            print(json.dumps({"bench": "kernels", **rec}), flush=True)
         return
     import torch
 
-    from nanovllm_amd import LLM, SamplingParams
     from nanovllm_amd import kernels
-    from nanovllm_amd.synthetic import default_aux_layers, write_eagle3_config, write_qwen3_config
 
     timer = AttnTimer()
     timer.wrap(kernels)
 
     tmp = tempfile.mkdtemp(prefix="nva_bench_")
-    target = write_qwen3_config(os.path.join(tmp, "target"), args.preset)
-    aux = default_aux_layers(args.preset)
-    draft = write_eagle3_config(os.path.join(tmp, "draft"), args.preset, aux_layers=aux)
-    max_len = args.prompt_max + args.max_tokens
-    blocks_per_seq = -(-(max_len + args.k + 1) // 256)
-    llm = LLM(target, load_format="dummy", seed=0, max_num_seqs=args.batch,
-              max_model_len=max_len, num_kvcache_blocks=args.batch * blocks_per_seq + 8,
-              max_num_batched_tokens=16384, enable_prefill_batching=True,
-              enforce_eager=args.eager, kv_cache_layout=args.kv_layout,
-              gemm_tuning_file=(args.gemm_tuning or None) if args.preset == "qwen3-8b" else None,
-              speculative_config={"method": "eagle3", "model": draft,
-                                  "num_speculative_tokens": args.k,
-                                  "aux_hidden_state_layers": aux})
+    llm = make_engine(args, tmp)
     runner = llm.model_runner
     log(f"engine up: {runner.get_diagnostics()}")
-    vocab = llm.config.hf_config.vocab_size
-    g = torch.Generator().manual_seed(args.seed)
-    lens = torch.randint(args.prompt_min, args.prompt_max + 1, (args.batch,), generator=g).tolist()
-    sp = SamplingParams(temperature=0.0, max_tokens=args.max_tokens, ignore_eos=True)
-    for L in lens:
-        llm.add_request(torch.randint(0, vocab, (L,), generator=g).tolist(), sp)
+    prompts = add_prompts(llm, args)
 
     t_setup = time.perf_counter()
     while llm.scheduler.waiting:
@@ -575,17 +860,8 @@ def main():
     runner.last_verify_inputs = None
 
     n_active = len(llm.scheduler.running)
-    before = dict(llm.spec_stats)
-    committed = 0
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        _, num_tokens = llm.step()
-        committed += -num_tokens
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    elapsed = t1 - t0
-    stats = {k: llm.spec_stats[k] - before[k] for k in before}
+    elapsed, committed, stats = timed_steps(llm, args.steps)
+    log(f"timed {args.steps} steps in {elapsed:.3f}s")
 
     # roofline: one more step of the same workload with the verify forward
     # launched eagerly (events cannot be recorded inside a captured HIP graph
@@ -598,36 +874,47 @@ def main():
     runner.use_verify_graph = True
     default_workload = all(getattr(args, key) == val for key, val in PMC_WORKLOAD.items())
     roof = timer.measure(args.roofline_repeats, PMC_TRAFFIC_BYTES if default_workload else None)
+    if roof is not None:
+        roof["traffic_source"] = (
+            "recorded constant (not measured by this run): rocprofv3 --pmc FETCH_SIZE then "
+            "WRITE_SIZE over `bench.py --attention-only` on this workload, scaled by the same "
+            "counters' readings for a 1 GiB device copy and a 1 GiB read; "
+            "profiles/verify_attention_traffic_qwen3_8b_bs64.md" if default_workload else
+            "not measured for this workload")
 
-    log(f"timed {args.steps} steps in {elapsed:.3f}s")
-    ref = None
+    # the target's greedy continuation of every sequence for the
+    # forced-acceptance run: the graphed steps commit exactly the target's
+    # argmax (the random draft is never accepted), so stepping on records it
+    continuations = None
+    if args.acceptance_steps > 0:
+        need = (3 + args.acceptance_steps + 2) * (args.k + 1)
+        while llm.scheduler.running and min(
+                s.num_completion_tokens for s in llm.scheduler.running) < need:
+            llm.step()
+        continuations = {tuple(s.prompt_token_ids): list(s.token_ids)
+                         for s in llm.scheduler.running}
+        if len(continuations) != len(prompts):
+            continuations = None   # a sequence finished (max_tokens too small)
+
+    ref = ref_torch = None
     if args.reference_steps > 0 and llm.scheduler.running:
-        # the reference's step structure on the same kernels and sequences:
-        # one warm-up step, then the timed ones
-        llm.reference_pipeline = True
-        llm.step()
-        torch.cuda.synchronize()
-        r0 = time.perf_counter()
-        ref_committed = 0
-        for _ in range(args.reference_steps):
-            _, num_tokens = llm.step()
-            ref_committed += -num_tokens
-        torch.cuda.synchronize()
-        r_el = time.perf_counter() - r0
-        llm.reference_pipeline = False
-        ref = {"value": round(ref_committed / r_el, 1), "unit": "tok/s",
-               "ms_per_step": round(r_el / args.reference_steps * 1e3, 2),
-               "steps": args.reference_steps,
-               "structure": "reference llm_engine.py:124-178 step shape on this build's kernels: "
-                            "eager draft loop with a host sync per draft step, eager target "
-                            "verify with one torch argmax + .tolist() per sequence, host "
-                            "acceptance per sequence, serial single-token draft replay per "
-                            "committed token (model_runner.py:1127-1156)"}
+        ref = reference_steps(llm, args.reference_steps, torch_attention=False)
         log(f"reference-structured steps: {ref['ms_per_step']} ms/step")
+        ref_torch = reference_steps(llm, args.reference_steps, torch_attention=True)
+        log(f"reference-structured steps, torch attention: {ref_torch['ms_per_step']} ms/step")
     cpu = None
     if cpu_batches:
         cpu = cpu_baseline(cpu_batches, args.cpu_seconds)
-    llm.exit()
+    release(llm)
+
+    forced = None
+    if continuations is not None:
+        forced = forced_acceptance(args, tmp, continuations)
+        log(f"forced acceptance: {forced['value']} tok/s, {forced['ms_per_step']} ms/step, "
+            f"mean acceptance length {forced['mean_acceptance_length']}")
+    per_config = None
+    if not args.no_per_config:
+        per_config = kernel_configs(args, 0.0 if args.no_cpu_baseline else 4.0)
 
     result = {
         "metric": METRIC,
@@ -652,10 +939,13 @@ def main():
                    "gemm_tuning": os.path.basename(args.gemm_tuning) if args.gemm_tuning else None},
         "roofline": roof,
         "cpu_baseline": cpu,
-        "reference_pipeline": ref,
         "committed_tokens": committed,
         "accepted_drafts_per_seq_step": round(stats["accepted"] / max(stats["steps"] * n_active, 1), 4),
         "committed_per_seq_step": round(stats["committed"] / max(stats["steps"] * n_active, 1), 4),
+        "forced_acceptance": forced,
+        "reference_pipeline": ref,
+        "reference_pipeline_torch_attention": ref_torch,
+        "per_config": per_config,
         "setup_s": round(setup_s, 1),
     }
     print(json.dumps(result), flush=True)

@@ -374,3 +374,35 @@ def test_scheduler_matches_reference_traces(index):
     for step, (got, want) in enumerate(zip(snaps, trace["snapshots"])):
         assert got == want, f"{trace['scenario']['name']} step {step}"
     assert final == trace["final_tokens"]
+
+
+@pytest.mark.parametrize("prefill", [True, False])
+def test_bench_torch_attention_matches_oracle(prefill):
+    """bench.py's torch stand-in for FlashAttention-2 (the comparator's
+    attention backend) computes the paged causal attention of the oracle:
+    bottom-right aligned verify rows, GQA, shuffled pages, ragged lengths;
+    and one row per sequence for the decode form.  Run on the CPU."""
+    from types import SimpleNamespace
+
+    import numpy as np
+
+    import bench
+    from helpers import bits, paged_case
+    from oracle import oracle
+
+    case = paged_case(seed=21, batch=4, q_len=[3, 1, 5, 2] if prefill else 1, ctx_lo=5,
+                      ctx_hi=700, hq=8, hkv=2)
+    layer = SimpleNamespace(k_cache=case["k_cache"], v_cache=case["v_cache"], scale=128 ** -0.5)
+    if prefill:
+        set_context(True, case["cu_q"], case["cu_k"], max(case["q_lens"]), int(case["lens"].max()),
+                    None, None, case["block_tables"])
+    else:
+        set_context(False, context_lens=case["lens"], block_tables=case["block_tables"])
+    try:
+        got = bench.TorchAttention().attend(layer, case["q"]).float().numpy()
+    finally:
+        reset_context()
+    ref = oracle.paged_attention(bits(case["q"]), bits(case["k_cache"]), bits(case["v_cache"]),
+                                 case["cu_q"].numpy(), case["lens"].numpy(),
+                                 case["block_tables"].numpy(), 128 ** -0.5)
+    assert np.abs(got - ref).max() <= 2e-2
