@@ -1,97 +1,134 @@
-"""Paged KV-cache block accounting with prefix caching
-(nanovllm/engine/block_manager.py:8-205).
+"""KV-cache page accounting with a prefix cache.
 
-Blocks hold ``block_size`` tokens.  A full block is identified by a chained
-xxhash64 of (previous block hash, its token ids) so identical prefixes can
-share physical blocks (reference-counted).  Speculative decoding adds
-``ensure_num_blocks_for_length`` (reserve draft positions before the draft
-writes K/V) and ``truncate`` (free the tail after rejection) -- the logical
-rollback that the device-side rollback kernel mirrors.
+Behaviour follows nanovllm/engine/block_manager.py:8-205.  Its observable
+state is pinned step by step by traces of the reference's own classes
+(tests/golden/scheduler_traces.json): the free list's order, reference
+counts, page keys and the key index.  The attribute names the traces read
+(``blocks``, ``free_block_ids``, ``used_block_ids``, ``hash_to_block_id``,
+``stats`` and the per-page fields) are kept for that reason.
+
+Model:
+  * a *page* is one physical block of ``block_size`` token slots;
+  * the *pool* hands out pages from the head of an ordered free list and
+    takes released pages back at its tail; a page's reference count is the
+    number of block tables holding it;
+  * a full page gets a *key*: xxhash64 chained over the previous page's key
+    (8 little-endian bytes) and its token ids (int64).  Once its K/V are
+    computed (``ready``) the key is *published* in the prefix index, and a
+    new sequence whose leading pages have the same keys and tokens reuses
+    them.  A released page keeps its key and content until the pool hands
+    it out again, so it can still be reused meanwhile.
+  * speculative decoding reserves pages for every draft position before the
+    draft writes K/V (``ensure_num_blocks_for_length``) and releases the
+    pages past the accepted length afterwards (``truncate``): the logical
+    rollback that the device-side rollback kernel mirrors.
 """
+from __future__ import annotations
+
 from collections import deque
+from dataclasses import dataclass, field
 
 import numpy as np
 import xxhash
 
 from nanovllm_amd.engine.sequence import Sequence
 
+NO_KEY = -1
 
-class Block:
 
-    def __init__(self, block_id: int):
-        self.block_id = block_id
-        self.ref_count = 0
-        self.hash = -1
-        self.token_ids: list[int] = []
-        self.ready = False
+def page_key(token_ids: list[int], prev_key: int = NO_KEY) -> int:
+    """xxhash64 of [prev_key as 8 little-endian bytes] + token ids as int64
+    (the prefix-cache key format, shared with the reference)."""
+    h = xxhash.xxh64()
+    if prev_key != NO_KEY:
+        h.update(prev_key.to_bytes(8, "little"))
+    h.update(np.asarray(token_ids, dtype=np.int64).tobytes())
+    return h.intdigest()
 
-    def update(self, h: int, token_ids: list[int]) -> None:
-        self.hash = h
-        self.token_ids = token_ids
 
-    def reset(self) -> None:
-        self.ref_count = 1
-        self.hash = -1
-        self.token_ids = []
-        self.ready = False
+@dataclass(slots=True)
+class Page:
+    block_id: int
+    ref_count: int = 0
+    hash: int = NO_KEY                     # the page key, once full
+    token_ids: list = field(default_factory=list)
+    ready: bool = False                    # K/V computed: reusable through the index
 
 
 class BlockManager:
 
+    compute_hash = staticmethod(page_key)
+
     def __init__(self, num_blocks: int, block_size: int, enable_prefix_caching: bool = True):
         self.block_size = block_size
         self.enable_prefix_caching = enable_prefix_caching
-        self.blocks = [Block(i) for i in range(num_blocks)]
-        self.hash_to_block_id: dict[int, int] = {}
+        self.blocks = [Page(i) for i in range(num_blocks)]
         self.free_block_ids: deque[int] = deque(range(num_blocks))
         self.used_block_ids: set[int] = set()
-        self.stats = {"prefix_cache_hits": 0, "prefix_cache_misses": 0, "reused_tokens": 0}
+        self.hash_to_block_id: dict[int, int] = {}
+        self.stats = dict.fromkeys(("prefix_cache_hits", "prefix_cache_misses",
+                                    "reused_tokens"), 0)
 
-    @classmethod
-    def compute_hash(cls, token_ids: list[int], prefix: int = -1) -> int:
-        """xxhash64 over the 8-byte little-endian prefix hash (when chained)
-        followed by the token ids as a native int64 array."""
-        h = xxhash.xxh64()
-        if prefix != -1:
-            h.update(prefix.to_bytes(8, "little"))
-        h.update(np.array(token_ids).tobytes())
-        return h.intdigest()
+    # ------------------------------------------------------------ pool
 
-    # ------------------------------------------------------------ internals
+    def _new_page(self) -> Page:
+        """The head of the free list, emptied, with one reference.  Its old
+        key stops pointing at it."""
+        page = self.blocks[self.free_block_ids.popleft()]
+        assert page.ref_count == 0
+        if page.hash != NO_KEY and self.hash_to_block_id.get(page.hash) == page.block_id:
+            del self.hash_to_block_id[page.hash]
+        page.ref_count, page.hash, page.token_ids, page.ready = 1, NO_KEY, [], False
+        self.used_block_ids.add(page.block_id)
+        return page
 
-    def _take(self, block_id: int) -> Block:
-        """Move a free block to the used set with a fresh single reference."""
-        block = self.blocks[block_id]
-        assert block.ref_count == 0
-        if block.hash != -1 and self.hash_to_block_id.get(block.hash) == block_id:
-            del self.hash_to_block_id[block.hash]
-        block.reset()
-        self.free_block_ids.remove(block_id)
-        self.used_block_ids.add(block_id)
-        return block
+    def _share(self, page: Page) -> None:
+        """One more table holds a cached page (taken off the free list if it
+        was released, content kept)."""
+        if page.block_id in self.used_block_ids:
+            page.ref_count += 1
+            return
+        self.free_block_ids.remove(page.block_id)
+        self.used_block_ids.add(page.block_id)
+        page.ref_count = 1
 
-    def _release(self, block_id: int) -> None:
-        assert self.blocks[block_id].ref_count == 0
-        self.used_block_ids.remove(block_id)
-        self.free_block_ids.append(block_id)
+    def _release(self, block_ids: list[int]) -> None:
+        """Drop one reference to each page, last page first; pages left with
+        none go to the tail of the free list."""
+        for block_id in reversed(block_ids):
+            page = self.blocks[block_id]
+            page.ref_count -= 1
+            if page.ref_count == 0:
+                self.used_block_ids.remove(block_id)
+                self.free_block_ids.append(block_id)
 
-    def _drop_ref(self, block_id: int) -> None:
-        block = self.blocks[block_id]
-        block.ref_count -= 1
-        if block.ref_count == 0:
-            self._release(block_id)
+    # ------------------------------------------------------------ keys
 
-    def _cached_block(self, h: int, token_ids: list[int]) -> int:
-        """Physical id of a ready block holding exactly these tokens, else -1."""
-        if not self.enable_prefix_caching or h == -1:
-            return -1
-        block_id = self.hash_to_block_id.get(h, -1)
-        if block_id == -1:
-            return -1
-        block = self.blocks[block_id]
-        if not block.ready or block.hash != h or block.token_ids != token_ids:
-            return -1
-        return block_id
+    def _publish(self, page: Page) -> None:
+        if self.enable_prefix_caching and page.ready:
+            self.hash_to_block_id[page.hash] = page.block_id
+
+    def _seal(self, seq: Sequence, index: int) -> None:
+        """Give page ``index`` of ``seq`` its key, chained on the previous
+        page's key."""
+        page = self.blocks[seq.block_table[index]]
+        prev = self.blocks[seq.block_table[index - 1]].hash if index else NO_KEY
+        page.token_ids = seq.page_tokens(index)
+        page.hash = page_key(page.token_ids, prev)
+
+    def _cached_prefix(self, pages: list[tuple[int, list[int]]]) -> int:
+        """Number of leading (key, tokens) pages of a new sequence that ready
+        cached pages hold exactly."""
+        if not self.enable_prefix_caching:
+            return 0
+        n = 0
+        for key, tokens in pages:
+            block_id = self.hash_to_block_id.get(key) if key != NO_KEY else None
+            page = self.blocks[block_id] if block_id is not None else None
+            if page is None or not page.ready or page.hash != key or page.token_ids != tokens:
+                break
+            n += 1
+        return n
 
     # ------------------------------------------------------------ prefill
 
@@ -99,109 +136,94 @@ class BlockManager:
         return len(self.free_block_ids) >= seq.num_blocks
 
     def allocate(self, seq: Sequence) -> None:
-        """Give a new sequence its block table, reusing cached prefix blocks
-        until the first miss."""
+        """Lay out a new sequence's block table: the longest run of leading
+        pages found in the prefix index is shared, every later page is new.
+        At least the last prompt token stays uncomputed (its logits are
+        needed), even when every page was cached."""
         assert not seq.block_table
-        h = -1
-        missed = False
+        pages, key = [], NO_KEY
         for i in range(seq.num_blocks):
-            token_ids = seq.block(i)
-            full = len(token_ids) == self.block_size
-            h = self.compute_hash(token_ids, h) if full else -1
-            block_id = -1 if missed else self._cached_block(h, token_ids)
-            if block_id == -1:
-                missed = True
-                if h != -1:
-                    self.stats["prefix_cache_misses"] += 1
-                block_id = self.free_block_ids[0]
-                block = self._take(block_id)
+            tokens = seq.page_tokens(i)
+            key = page_key(tokens, key) if len(tokens) == self.block_size else NO_KEY
+            pages.append((key, tokens))
+        hits = self._cached_prefix(pages)
+        for i, (key, tokens) in enumerate(pages):
+            if i < hits:
+                page = self.blocks[self.hash_to_block_id[key]]
+                self._share(page)
             else:
-                seq.num_cached_tokens += self.block_size
-                self.stats["prefix_cache_hits"] += 1
-                self.stats["reused_tokens"] += self.block_size
-                block = self.blocks[block_id]
-                if block_id in self.used_block_ids:
-                    block.ref_count += 1
-                else:
-                    self.free_block_ids.remove(block_id)
-                    self.used_block_ids.add(block_id)
-                    block.ref_count = 1
-            if h != -1:
-                block.update(h, token_ids)
-                if self.enable_prefix_caching and block.ready:
-                    self.hash_to_block_id[h] = block_id
-            seq.block_table.append(block_id)
-        # at least the last prompt token is recomputed to produce logits
-        seq.num_computed_tokens = min(seq.num_cached_tokens, max(seq.num_tokens - 1, 0))
+                page = self._new_page()
+                if key != NO_KEY:
+                    self.stats["prefix_cache_misses"] += 1
+                    page.hash, page.token_ids = key, tokens
+            seq.block_table.append(page.block_id)
+        self.stats["prefix_cache_hits"] += hits
+        self.stats["reused_tokens"] += hits * self.block_size
+        seq.num_cached_tokens += hits * self.block_size
+        seq.num_computed_tokens = min(seq.num_cached_tokens, max(len(seq) - 1, 0))
 
     def mark_computed(self, seq: Sequence) -> None:
-        """Blocks fully covered by computed tokens become reusable."""
+        """Pages wholly covered by computed tokens become ready (keyed first
+        if they are not yet) and are published."""
         full = min(seq.num_computed_tokens // self.block_size, len(seq.block_table))
         for index in range(full):
-            block = self.blocks[seq.block_table[index]]
-            if block.ready:
+            page = self.blocks[seq.block_table[index]]
+            if page.ready:
                 continue
-            if block.hash == -1:
-                prefix = self.blocks[seq.block_table[index - 1]].hash if index > 0 else -1
-                token_ids = seq.block(index)
-                block.update(self.compute_hash(token_ids, prefix), token_ids)
-            block.ready = True
-            if self.enable_prefix_caching:
-                self.hash_to_block_id[block.hash] = block.block_id
+            if page.hash == NO_KEY:
+                self._seal(seq, index)
+            page.ready = True
+            self._publish(page)
 
     def deallocate(self, seq: Sequence) -> None:
-        for block_id in reversed(seq.block_table):
-            self._drop_ref(block_id)
-        seq.num_cached_tokens = 0
-        seq.num_computed_tokens = 0
-        seq.num_scheduled_tokens = 0
+        self._release(seq.block_table)
         seq.block_table.clear()
+        seq.num_cached_tokens = seq.num_computed_tokens = seq.num_scheduled_tokens = 0
 
     # ------------------------------------------------------------ decode
 
     def can_append(self, seq: Sequence) -> bool:
-        return len(self.free_block_ids) >= (len(seq) % self.block_size == 1)
+        """Room for the token just appended: a length of k*block_size + 1
+        opens a page."""
+        opens_page = len(seq) % self.block_size == 1
+        return len(self.free_block_ids) >= int(opens_page)
 
     def may_append(self, seq: Sequence) -> None:
-        """Keep the block table consistent after one token was appended.
-
-        A length of k*block_size + 1 needs a new block (unless speculation
-        already reserved it); a length of k*block_size finalises (hashes) the
-        last block unless that already happened."""
-        table = seq.block_table
-        last = self.blocks[table[-1]]
-        rem = len(seq) % self.block_size
-        if rem == 1:
-            if len(table) >= seq.num_blocks:
-                return
-            assert last.hash != -1
-            block = self._take(self.free_block_ids[0])
-            table.append(block.block_id)
-        elif rem == 0:
-            if last.hash != -1:
-                return
-            token_ids = seq.block(seq.num_blocks - 1)
-            prefix = self.blocks[table[-2]].hash if len(table) > 1 else -1
-            h = self.compute_hash(token_ids, prefix)
-            last.update(h, token_ids)
-            if self.enable_prefix_caching and last.ready:
-                self.hash_to_block_id[h] = last.block_id
+        """Keep the table in step with a sequence that just grew by one token.
+        Both cases are idempotent, because speculation may have reserved the
+        next page or sealed the last one already:
+          length % block_size == 1: the new token opens a page;
+          length % block_size == 0: the last page is full and gets its key."""
+        last = self.blocks[seq.block_table[-1]]
+        offset = len(seq) % self.block_size
+        if offset == 1:
+            if len(seq.block_table) < seq.num_blocks:
+                assert last.hash != NO_KEY
+                seq.block_table.append(self._new_page().block_id)
+        elif offset == 0:
+            if last.hash == NO_KEY:
+                table = seq.block_table
+                prev = self.blocks[table[-2]].hash if len(table) > 1 else NO_KEY
+                last.token_ids = seq.page_tokens(seq.num_blocks - 1)
+                last.hash = page_key(last.token_ids, prev)
+                self._publish(last)
         else:
-            assert last.hash == -1
+            assert last.hash == NO_KEY
 
     # ------------------------------------------------------------ speculation
 
     def ensure_num_blocks_for_length(self, seq: Sequence, num_tokens: int) -> None:
-        """Reserve blocks for ``num_tokens`` tokens before draft K/V is written."""
-        need = -(-num_tokens // self.block_size)
-        while len(seq.block_table) < need:
+        """Reserve pages for ``num_tokens`` tokens before the draft writes K/V
+        for positions not yet committed."""
+        missing = -(-num_tokens // self.block_size) - len(seq.block_table)
+        for _ in range(missing):
             if not self.free_block_ids:
                 raise RuntimeError("not enough KV-cache blocks for speculative proposal")
-            seq.block_table.append(self._take(self.free_block_ids[0]).block_id)
+            seq.block_table.append(self._new_page().block_id)
 
     def truncate(self, seq: Sequence) -> None:
-        """Release blocks beyond the sequence's current length."""
+        """Release the pages past the sequence's current length (rejected
+        draft positions)."""
         keep = seq.num_blocks
-        for block_id in reversed(seq.block_table[keep:]):
-            self._drop_ref(block_id)
+        self._release(seq.block_table[keep:])
         del seq.block_table[keep:]

@@ -321,8 +321,7 @@ class ModelRunner:
         input_ids = [seq.last_token for seq in seqs]
         positions = [len(seq) - 1 for seq in seqs]
         context_lens = [len(seq) for seq in seqs]
-        slots = [seq.block_table[-1] * self.block_size + seq.last_block_num_tokens - 1
-                 for seq in seqs]
+        slots = [self._slot(seq, p) for seq, p in zip(seqs, positions)]
         dev = self.device
         cu_q = list(range(len(seqs) + 1))
         cu_k = [0]
