@@ -83,6 +83,14 @@ def parse_args():
                          "the target's greedy token")
     ap.add_argument("--no-per-config", action="store_true",
                     help="skip the per-config kernel figures of the JSON line")
+    ap.add_argument("--profile-steps", type=int, default=0,
+                    help="after the timed steps, run this many more steps between two marker "
+                         "kernels (torch spin_kernel), to cut a rocprofv3 kernel trace to "
+                         "steady-state steps")
+    ap.add_argument("--workload", default="config3", choices=["config3", "config5"],
+                    help="config3: the default bench line (BASELINE config 3); config5: the "
+                         "Qwen3-32B-geometry engine run of BASELINE config 5 (k=7, B128, "
+                         "contexts U[2048, 8192], shuffled pages), its own JSON line")
     ap.add_argument("--gemm-tuning", default=DEFAULT_GEMM_TUNING,
                     help="TunableOp results for the projection GEMMs ('' for library defaults)")
     ap.add_argument("--kv-layout", default="head_major", choices=["head_major", "token_major"],
@@ -91,6 +99,8 @@ def parse_args():
                     help="time each hot-path kernel alone on the seeded synthetic inputs of "
                          "BASELINE configs 1, 2, 4 and 5 (and config 3's shapes); one JSON line "
                          "per kernel and config")
+    ap.add_argument("--kernel-filter", default="",
+                    help="--kernels: only the records whose config name contains this text")
     ap.add_argument("--batch-order", default="longest_first", choices=["longest_first", "drawn"],
                     help="--kernels: sequences longest first (the engine's verify order) or "
                          "in the order drawn")
@@ -471,6 +481,9 @@ def kernel_configs(args, cpu_seconds: float = 0.0) -> list:
 
     records = []
 
+    def wanted(config):
+        return args.kernel_filter in config
+
     def emit(kernel, config, us, byts, **extra):
         gbs = byts / us / 1e3
         records.append({"kernel": kernel, "config": config, "us": round(us, 2),
@@ -617,36 +630,49 @@ def kernel_configs(args, cpu_seconds: float = 0.0) -> list:
         emit("K4 argmax_accept", name, us, batch * q_len * V * 2, rows=batch * q_len, vocab=V,
              **extra)
 
-    acceptance("config1 B8 k4", 0, 8, 4)
-    acceptance("config3 verify rows B64 k5", 2, 64, 5)
+    if wanted("config1 B8 k4"):
+        acceptance("config1 B8 k4", 0, 8, 4)
+    if wanted("config3 verify rows B64 k5"):
+        acceptance("config3 verify rows B64 k5", 2, 64, 5)
 
-    c2 = pages(1, 32, 5, 512, 4096, 16, 8, copies=4)
-    store("config2 B32 q5", c2)
-    attention("config2 B32 q5 Qwen3-0.6B", c2)
-    rollback("config2 B32 q5", c2)
-    del c2
+    if wanted("config2 B32 q5"):
+        c2 = pages(1, 32, 5, 512, 4096, 16, 8, copies=4)
+        store("config2 B32 q5", c2)
+        attention("config2 B32 q5 Qwen3-0.6B", c2)
+        rollback("config2 B32 q5", c2)
+        del c2
 
-    c3 = pages(2, 64, 6, 256, 2304, 32, 8, copies=4)
-    store("config3 B64 q6", c3)
-    attention("config3 B64 q6 Qwen3-8B", c3)
-    H = QWEN3_PRESETS["qwen3-8b"]["hidden_size"]
-    hid = [torch.randn(c3["T"], H, device=dev).to(torch.bfloat16) for _ in range(3)]
-    res = [torch.randn(c3["T"], H, device=dev).to(torch.bfloat16) for _ in range(3)]
-    src = torch.arange(c3["T"], dtype=torch.int32, device=dev)
-    us = timed(lambda: kernels.aux_gather(hid, res, src))
-    emit("K3 aux_gather", "config3 R=384 H=4096 3 layers", us, c3["T"] * 3 * H * 2 * 3)
-    dec = pages(5, 64, 1, 256, 2304, 32, 8, copies=4)
-    attention("config3 draft decode B64 q1", dec)
-    del c3, dec, hid, res
+    if wanted("config3 B64 q6"):
+        c3 = pages(2, 64, 6, 256, 2304, 32, 8, copies=4)
+        store("config3 B64 q6", c3)
+        attention("config3 B64 q6 Qwen3-8B", c3)
+        H = QWEN3_PRESETS["qwen3-8b"]["hidden_size"]
+        hid = [torch.randn(c3["T"], H, device=dev).to(torch.bfloat16) for _ in range(3)]
+        res = [torch.randn(c3["T"], H, device=dev).to(torch.bfloat16) for _ in range(3)]
+        src = torch.arange(c3["T"], dtype=torch.int32, device=dev)
+        us = timed(lambda: kernels.aux_gather(hid, res, src))
+        emit("K3 aux_gather", "config3 B64 q6 R=384 H=4096 3 layers", us, c3["T"] * 3 * H * 2 * 3)
+        del c3, hid, res
+    if wanted("config3 draft decode B64 q1"):
+        dec = pages(5, 64, 1, 256, 2304, 32, 8, copies=4)
+        attention("config3 draft decode B64 q1", dec)
+        del dec
 
-    c4 = pages(3, 128, 5, 4096, 16384, 16, 8, fp8=True)
-    store("config4 B128 q5 fp8", c4)
-    attention("config4 B128 q5 fp8", c4)
-    del c4
+    if wanted("config4 B128 q5 fp8"):
+        c4 = pages(3, 128, 5, 4096, 16384, 16, 8, fp8=True)
+        store("config4 B128 q5 fp8", c4)
+        attention("config4 B128 q5 fp8", c4)
+        del c4
 
-    c5 = pages(4, 128, 8, 2048, 8192, 64, 8, shared_frac=0.3)
-    attention("config5 B128 q8 Qwen3-32B (30% shared prefix pages)", c5)
-    del c5
+    if wanted("config5 B128 q8"):
+        c5 = pages(4, 128, 8, 2048, 8192, 64, 8, shared_frac=0.3)
+        attention("config5 B128 q8 Qwen3-32B (30% shared prefix pages)", c5)
+        del c5
+    if wanted("config5 draft decode B128 q1"):
+        # the draft's one-layer cache: one query row per sequence, 64 q heads
+        d5 = pages(6, 128, 1, 2048, 8192, 64, 8)
+        attention("config5 draft decode B128 q1 Qwen3-32B", d5)
+        del d5
     torch.cuda.empty_cache()
     return records
 
@@ -698,6 +724,25 @@ def release(llm) -> None:
     del llm
     gc.collect()
     torch.cuda.empty_cache()
+
+
+def profiled_steps(llm, steps: int) -> None:
+    """``steps`` more engine steps between two marker kernels (torch's
+    spin_kernel, launched only here), so that a `rocprofv3 --kernel-trace`
+    record can be cut to exactly these steady-state steps."""
+    import torch
+
+    if steps <= 0:
+        return
+    torch.cuda.synchronize()
+    torch.cuda._sleep(1000)
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        llm.step()
+    torch.cuda.synchronize()
+    torch.cuda._sleep(1000)
+    torch.cuda.synchronize()
+    log(f"{steps} profiled steps done (between two spin_kernel markers)")
 
 
 def timed_steps(llm, steps: int):
@@ -802,6 +847,145 @@ def forced_acceptance(args, tmp: str, continuations):
                       "probability draft_keep"}
 
 
+def config5(args) -> None:
+    """BASELINE config 5 through the engine: Qwen3-32B geometry (64 layers,
+    H5120, 64 q / 8 kv heads, MLP 25600, V151936, random weights), an EAGLE3
+    draft with k = 7 (8 verify rows per sequence, 64-row attention tiles),
+    128 sequences with prompts of U[2048, 8192] random tokens (seed 4).  The
+    pool's free list is shuffled (seeded), so block tables are fragmented.
+    The config's 30% prefix-shared pages are a kernel-level property (the
+    per-config K1 figure reads them): the engine, like the reference
+    (config.py:150), turns prefix caching off with EAGLE3, because the
+    draft's K/V at a page's last position depends on the next page's first
+    token.  Without sharing the pages take ~198 GB next to 70 GB of weights.
+    Prints one JSON line: step time and accepted tok/s over the timed steps
+    (zero acceptance with random weights), the verify attention of one step
+    re-issued between HIP events, and a greedy check of 4 sequences
+    (teacher-forced prefill of prompt + output: every output token within
+    16 bf16 ulps of the row's top logit)."""
+    from collections import deque
+
+    import torch
+
+    from nanovllm_amd import LLM, SamplingParams
+    from nanovllm_amd import kernels
+    from nanovllm_amd.context import reset_context
+    from nanovllm_amd.engine.sequence import Sequence
+    from nanovllm_amd.synthetic import default_aux_layers, write_eagle3_config, write_qwen3_config
+
+    preset, batch, k, block = "qwen3-32b", 128, 7, 256
+    lo, hi, seed = 2048, 8192, 4
+    timer = AttnTimer()
+    timer.wrap(kernels)
+    tmp = tempfile.mkdtemp(prefix="nva_c5_")
+    target = write_qwen3_config(os.path.join(tmp, "target"), preset)
+    aux = default_aux_layers(preset)
+    draft = write_eagle3_config(os.path.join(tmp, "draft"), preset, aux_layers=aux)
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(lo, hi + 1, (batch,), generator=g).tolist()
+    prompts = [torch.randint(0, 151936, (L,), generator=g).tolist() for L in lens]
+    # one token per step at zero acceptance: the decode steps that alternate
+    # with the ~40 prefill steps (16k tokens each), warm-up, timed and
+    # roofline steps, and the k draft positions reserved ahead; the pool
+    # also holds the greedy check's probe (its own full table)
+    gen = 48 + args.warmup + args.steps + args.profile_steps + 2 + k + 1
+    max_len = hi + gen
+    pages = sum(-(-(L + gen) // block) for L in lens) + -(-max_len // block) + 8
+    t0 = time.perf_counter()
+    llm = LLM(target, load_format="dummy", seed=0, max_num_seqs=batch, max_model_len=max_len,
+              num_kvcache_blocks=pages, max_num_batched_tokens=16384,
+              enable_prefill_batching=True, gpu_memory_utilization=0.97,
+              kv_cache_layout=args.kv_layout,
+              speculative_config={"method": "eagle3", "model": draft,
+                                  "num_speculative_tokens": k, "aux_hidden_state_layers": aux})
+    runner = llm.model_runner
+    bm = llm.scheduler.block_manager
+    total = len(bm.blocks)
+    bm.free_block_ids = deque(torch.randperm(total, generator=g).tolist())
+    log(f"config5 engine up in {time.perf_counter() - t0:.1f}s ({total} of {pages} pages): "
+        f"{runner.get_diagnostics()}")
+    sp = SamplingParams(temperature=0.0, max_tokens=gen, ignore_eos=True)
+    t0 = time.perf_counter()
+    for p in prompts:
+        llm.add_request(p, sp)
+    steps = 0
+    while llm.scheduler.waiting:
+        llm.step()
+        steps += 1
+        if steps % 8 == 0:
+            log(f"config5 prefill: {len(llm.scheduler.waiting)} waiting after {steps} steps")
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    log(f"config5 prefill done in {prefill_s:.1f}s ({steps} steps)")
+    for _ in range(args.warmup):
+        llm.step()
+    n_active = len(llm.scheduler.running)
+    elapsed, committed, stats = timed_steps(llm, args.steps)
+    ctx = [len(s) + k + 1 for s in llm.scheduler.running]
+    log(f"config5 timed {args.steps} steps in {elapsed:.3f}s")
+    profiled_steps(llm, args.profile_steps)
+    # the verify attention of one more step, re-issued between HIP events
+    orig_verify = runner.verify_eagle3_batch_fused
+
+    def verify_with_lens(seqs, n):
+        timer.current_lens = [len(x) for x in seqs]
+        try:
+            return orig_verify(seqs, n)
+        finally:
+            timer.current_lens = None
+
+    runner.verify_eagle3_batch_fused = verify_with_lens
+    runner.use_verify_graph = False
+    timer.capture = True
+    llm.step()
+    timer.capture = False
+    runner.use_verify_graph = True
+    runner.verify_eagle3_batch_fused = orig_verify
+    roof = timer.measure(2, None)
+    # greedy check of 4 sequences (the longest among them) by teacher forcing
+    running = list(llm.scheduler.running)
+    picks = sorted(running, key=lambda x: -len(x))[:1] + running[:3]
+    worst, checked = 0.0, 0
+    for seq in picks:
+        toks = list(seq.token_ids)
+        start = seq.num_prompt_tokens
+        probe = Sequence(toks)
+        bm.allocate(probe)
+        probe.num_computed_tokens = 0
+        probe.num_scheduled_tokens = len(toks)
+        try:
+            with torch.inference_mode():
+                ids, pos = runner.prepare_prefill([probe])
+                hidden = runner.model(ids, pos)
+                rows = runner.model.compute_all_logits(hidden[start - 1:len(toks) - 1]).float()
+        finally:
+            reset_context()
+            bm.deallocate(probe)
+        top = rows.max(-1).values
+        got = rows.gather(1, torch.tensor(toks[start:], device=rows.device)[:, None])[:, 0]
+        ulp = torch.exp2(torch.floor(torch.log2(top.abs())) - 7)
+        gaps = ((top - got) / ulp).cpu()
+        worst = max(worst, float(gaps.max()))
+        checked += gaps.numel()
+    release(llm)
+    seq_steps = max(stats["steps"] * n_active, 1)
+    print(json.dumps({
+        "workload": "BASELINE config 5 through LLM: Qwen3-32B geometry (64 layers, H5120, "
+                    "64q/8kv, D128, MLP25600, V151936), EAGLE3 draft k=7, random weights, "
+                    "shuffled pages (no prefix sharing with EAGLE3, as in the reference)",
+        "batch": n_active, "k": k, "steps": args.steps, "warmup": args.warmup,
+        "value": round(committed / elapsed, 1), "unit": "tok/s",
+        "ms_per_step": round(elapsed / args.steps * 1e3, 2),
+        "committed_per_seq_step": round(stats["committed"] / seq_steps, 4),
+        "context_len": [min(ctx), max(ctx), round(sum(ctx) / len(ctx))],
+        "prefill_s": round(prefill_s, 1), "pages": total,
+        "verify_attention": roof,
+        "greedy_check": {"sequences": len(picks), "tokens": checked,
+                         "max_gap_ulps": round(worst, 1), "tolerance_ulps": 16,
+                         "ok": worst < 16},
+    }), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -814,6 +998,9 @@ def main():
     if args.kernels:
         for rec in kernel_configs(args, 0.0 if args.no_cpu_baseline else 4.0):
             print(json.dumps({"bench": "kernels", **rec}), flush=True)
+        return
+    if args.workload == "config5":
+        config5(args)
         return
     import torch
 
@@ -862,6 +1049,7 @@ def main():
     n_active = len(llm.scheduler.running)
     elapsed, committed, stats = timed_steps(llm, args.steps)
     log(f"timed {args.steps} steps in {elapsed:.3f}s")
+    profiled_steps(llm, args.profile_steps)
 
     # roofline: one more step of the same workload with the verify forward
     # launched eagerly (events cannot be recorded inside a captured HIP graph

@@ -869,15 +869,40 @@ int32_t choose_qtile(int32_t max_q, int32_t group) {
   return max_q < qtile ? (max_q > 0 ? max_q : 1) : qtile;
 }
 
-// Split length: 384 keys per wave when several waves share a split (3072
-// for eight, each wave walking every eighth chunk), 3072 keys when one wave
-// runs it (64-row tiles, FP8 tiles beyond the stream decomposition): most
-// verify sequences then need a single split and no combine, and long ones
-// write few fp32 partials.  Measured on MI355X, longest-first batches:
-// Qwen3-8B verify (24-row tiles, ~1.2k keys) eight waves on 3072 keys
-// 66.0 us per call against four on 1536 68.6 us; Qwen3-32B verify (64-row
-// tiles, 2-8k keys) one wave on 3072 keys 543 us against 648 us on 768 and
-// 566 us on 4096.  The length shrinks in 128-key steps (to a 128-key
+// Compute units of the current device (cached per device; 256 when the
+// query fails).
+int32_t device_cus() {
+  static int32_t cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        n <= 0)
+      n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+// Split length of the fixed decomposition.  A segment is one (sequence, kv
+// head, query tile); `waves` waves share each split.
+//   * Eight waves per split (bf16 tiles of up to 32 rows): 384 keys per
+//     wave, 3072 per split; when the batch has at least four segments per
+//     CU (several rounds of workgroups, which the dispatcher balances), one
+//     split covers the whole sequence instead (no fp32 partials, no
+//     combine, each workgroup streams longer).
+//   * One wave per split (64-row tiles, FP8 tiles off the stream path):
+//     3072 keys; with at least one segment per SIMD, about three quarters of
+//     the longest sequence (a multiple of 1024), so that only the longest
+//     sequences split in two: fewer, longer waves, while the trailing
+//     splits still fill in behind the first round.
+// Measured on MI355X (bench.py --kernels, NVA_ATTN_SPLIT_KEYS sweeps in one
+// run): Qwen3-32B verify (64-row tiles, keys 2-8k) 521 us at 3072, 545 at
+// 4096, 484-487 at 6144, 590 at 8192 (one round of unequal waves); Qwen3-32B
+// draft decode (8-row tiles, 1024 segments) 431 us at 3072, 414 whole;
+// Qwen3-0.6B verify (256 segments, one round, keys up to 4k) 60.2 us at
+// 3072 against 64.3 whole (the longest segments alone set the time).  The length shrinks in 128-key steps (to a 128-key
 // minimum) only while fewer than kMinWaves waves would be launched, and is
 // capped so that a split spans at most kWave - 2 blocks of block_size tokens
 // (the kernel holds one block id per lane); block_size 0 (unknown: the
@@ -885,11 +910,21 @@ int32_t choose_qtile(int32_t max_q, int32_t group) {
 // the split count from above.
 void choose_split(int32_t num_seqs, int32_t num_kv_heads, int32_t n_qtiles, int32_t max_k,
                   int32_t waves, int32_t block_size, int32_t* split_len, int32_t* max_splits) {
-  const int64_t base = static_cast<int64_t>(num_seqs > 0 ? num_seqs : 1) *
-                       (num_kv_heads > 0 ? num_kv_heads : 1) * (n_qtiles > 0 ? n_qtiles : 1) *
-                       (waves > 0 ? waves : 1);
+  const int64_t segs = static_cast<int64_t>(num_seqs > 0 ? num_seqs : 1) *
+                       (num_kv_heads > 0 ? num_kv_heads : 1) * (n_qtiles > 0 ? n_qtiles : 1);
+  const int64_t base = segs * (waves > 0 ? waves : 1);
   const int32_t mk = max_k > 1 ? max_k : 1;
-  int32_t len = waves > 1 ? kKeysPerSharedWave * waves : kSplitKeys;
+  const int32_t cus = device_cus();
+  int32_t len;
+  if (waves > 1) {
+    len = kKeysPerSharedWave * waves;
+    const int32_t whole = (mk + kMinSplit - 1) / kMinSplit * kMinSplit;
+    if (segs >= 4 * static_cast<int64_t>(cus) && whole > len) len = whole;
+  } else {
+    len = kSplitKeys;
+    const int32_t most = 3 * (mk / 4) / 1024 * 1024;
+    if (segs >= 4 * static_cast<int64_t>(cus) && most > len) len = most;
+  }
   const int32_t span = (kWave - 2) * (block_size > 0 ? block_size : kChunk);
   if (len > span) len = span / kMinSplit * kMinSplit;
   while (len > kMinSplit && base * ((mk + len - 1) / len) < kMinWaves) len -= kMinSplit;
@@ -960,21 +995,15 @@ int32_t stream_max_splits(int32_t max_k) {
   return (chunks + kMinRangeChunks - 1) / kMinRangeChunks + 1;
 }
 
-// Stream workgroups per kv head: one wave per SIMD of the device (cached).
+// Stream workgroups per kv head: one wave per SIMD of the device.
 int32_t stream_ranges_per_head(int32_t hkv) {
-  static int32_t simds[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (simds[dev] == 0) {
-    int cus = 0;
-    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
-      cus = 256;
-    int per_simd = 1;
-    if (const char* v = getenv("NVA_ATTN_STREAM_WAVES")) per_simd = atoi(v) > 0 ? atoi(v) : 1;
-    simds[dev] = cus * 4 * per_simd;
-  }
+  static const int per_simd = [] {
+    const char* v = getenv("NVA_ATTN_STREAM_WAVES");
+    return v && atoi(v) > 0 ? atoi(v) : 1;
+  }();
+  const int32_t simds = device_cus() * 4 * per_simd;
   const int32_t h = hkv > 0 ? hkv : 1;
-  return (simds[dev] + h - 1) / h;
+  return (simds + h - 1) / h;
 }
 
 // Workspace for either KV dtype (the size query does not name one): the

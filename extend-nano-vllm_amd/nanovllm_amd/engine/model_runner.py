@@ -412,6 +412,19 @@ class ModelRunner:
                                         | set(getattr(self, "_propose_graphs", {}))),
         }
 
+    def _draft_step_metadata(self, seqs: list[Sequence], limits: list[int], steps: int):
+        """Per draft step s < steps - 1 and sequence i: the RoPE position
+        len_i - 1 + s, the slot its K/V goes to, and the keys it sees.  A
+        sequence that needs fewer proposals (limits[i] < steps, near its
+        max_tokens) gets slot -1 in the steps past its own last one: those
+        steps' tokens are discarded, and their positions may lie beyond the
+        pages reserved for it (reserve_speculation stops at max_tokens)."""
+        pos = [[len(seq) - 1 + s for seq in seqs] for s in range(steps - 1)]
+        slots = [[self._slot(seq, p) if s < lim - 1 else -1
+                  for seq, p, lim in zip(seqs, row, limits)] for s, row in enumerate(pos)]
+        ctx_lens = [[p + 1 for p in row] for row in pos]
+        return pos, slots, ctx_lens
+
     def _use_graphs(self) -> bool:
         return not self.enforce_eager
 
@@ -429,9 +442,7 @@ class ModelRunner:
         if steps <= 0:
             return [[] for _ in seqs]
         lens = [len(seq) for seq in seqs]
-        pos = [[n - 1 + s for n in lens] for s in range(steps - 1)]
-        slots = [[self._slot(seq, p) for seq, p in zip(seqs, row)] for row in pos]
-        ctx_lens = [[p + 1 for p in row] for row in pos]
+        pos, slots, ctx_lens = self._draft_step_metadata(seqs, limits, steps)
         state_rows = _pinned(self._state_rows(seqs), torch.int64).to(self.device, non_blocking=True)
         bs = bucket_for(len(seqs))
         if self._use_graphs() and steps == k and bs is not None:
@@ -485,9 +496,7 @@ class ModelRunner:
         if steps <= 0:
             return [[] for _ in seqs]
         lens = [len(seq) for seq in seqs]
-        pos = [[n - 1 + s for n in lens] for s in range(steps - 1)]
-        slots = [[self._slot(seq, p) for seq, p in zip(seqs, row)] for row in pos]
-        ctx_lens = [[p + 1 for p in row] for row in pos]
+        pos, slots, ctx_lens = self._draft_step_metadata(seqs, limits, steps)
         state_rows = _pinned(self._state_rows(seqs), torch.int64).to(self.device, non_blocking=True)
         table = self._propose_eager(seqs, state_rows, steps, pos, slots, ctx_lens, lens,
                                     sync_each_step=True)
@@ -565,9 +574,7 @@ class ModelRunner:
                 or any(seq.max_tokens - seq.num_completion_tokens < k for seq in seqs)):
             return None
         lens = [len(seq) for seq in seqs]
-        pos = [[n - 1 + s for n in lens] for s in range(k - 1)]
-        slots = [[self._slot(seq, p) for seq, p in zip(seqs, row)] for row in pos]
-        ctx_lens = [[p + 1 for p in row] for row in pos]
+        pos, slots, ctx_lens = self._draft_step_metadata(seqs, [k] * b, k)
         state_rows = _pinned(self._state_rows(seqs), torch.int64).to(self.device, non_blocking=True)
         pgraph = self._propose_graphs.get(bs)
         if pgraph is None:

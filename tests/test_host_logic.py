@@ -406,3 +406,33 @@ def test_bench_torch_attention_matches_oracle(prefill):
                                  case["cu_q"].numpy(), case["lens"].numpy(),
                                  case["block_tables"].numpy(), 128 ** -0.5)
     assert np.abs(got - ref).max() <= 2e-2
+
+
+def test_draft_steps_past_a_sequence_limit_write_nowhere(cpu_runner):
+    """A batch mixing a sequence near max_tokens (one proposal left, its
+    pages reserved only up to prompt + max_tokens) with one that drafts k:
+    the draft steps past the short sequence's own last step get slot -1 (no
+    K/V write, no page lookup past its table), the others their slots."""
+    sched = _scheduler(k=5)
+    near = Sequence(list(range(253)), SamplingParams(temperature=0.0, max_tokens=2,
+                                                     ignore_eos=True))
+    far = Sequence(list(range(1000, 1040)), SamplingParams(temperature=0.0, max_tokens=64,
+                                                           ignore_eos=True))
+    sched.add(near)
+    sched.add(far)
+    seqs, is_prefill = sched.schedule()                   # prefill batching: both
+    assert is_prefill and seqs == [near, far]
+    sched.postprocess(seqs, [1, 1], True)                 # near: len 254, one token left
+    sched.schedule()
+    for seq in (near, far):
+        sched.reserve_speculation(seq)
+    assert len(near.block_table) == 1          # 253 + 2 tokens fit page 0
+    with pytest.raises(IndexError):            # position 256 has no page
+        cpu_runner._slot(near, 256)
+    limits = [min(5, s.max_tokens - s.num_completion_tokens) for s in (near, far)]
+    assert limits == [1, 5]
+    pos, slots, ctx = cpu_runner._draft_step_metadata([near, far], limits, 5)
+    assert [row[0] for row in pos] == [253, 254, 255, 256]
+    assert [row[0] for row in slots] == [-1, -1, -1, -1]
+    assert [row[1] for row in slots] == [far.block_table[0] * BS + p for p in (40, 41, 42, 43)]
+    assert [row[1] for row in ctx] == [41, 42, 43, 44]
