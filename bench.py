@@ -40,15 +40,15 @@ DEFAULT_GEMM_TUNING = os.path.join(ROOT, "extend-nano-vllm_amd", "nanovllm_amd",
                                    "gemm_mi355x_qwen3_8b_eagle3.csv")
 
 # HBM bytes per verify-attention call on this workload, from two rocprofv3
-# --pmc runs of `bench.py --attention-only` (FETCH_SIZE, then WRITE_SIZE;
-# KiB per dispatch, averaged over the 75 calls of `--attention-only
-# --roofline-repeats 2`), scaled by what the same counters read for a 1 GiB
-# device copy in the same runs: FETCH_SIZE 524301 KiB (x2.0 to bytes read),
-# WRITE_SIZE 1048576 KiB (x1.0).  attention kernel: FETCH 158667.1, WRITE
+# --pmc runs of `bench.py --attention-only --roofline-repeats 2` (FETCH_SIZE,
+# then WRITE_SIZE; KiB per dispatch, mean of the 75 calls), scaled by what
+# the same counters read for a 1 GiB device copy and a 1 GiB read in the same
+# runs: FETCH_SIZE 524307 / 524348 KiB (x2.0 to bytes read), WRITE_SIZE
+# 1048576 KiB for the copy (x1.0).  Attention kernel: FETCH 158671.6, WRITE
 # 3072.0 (no sequence of this workload needs a second split, so no combine
-# kernel runs).  Only quoted for the default workload, whose shapes it was
-# measured on.
-PMC_TRAFFIC_BYTES = int((158667.1 * 2.0 + 3072.0 * 1.0) * 1024)
+# kernel runs).  A recorded constant, quoted only for the default workload,
+# whose shapes it was measured on.
+PMC_TRAFFIC_BYTES = int((158671.6 * 2.0 + 3072.0 * 1.0) * 1024)
 PMC_WORKLOAD = dict(preset="qwen3-8b", batch=64, k=5, prompt_min=256, prompt_max=2048,
                     max_tokens=256, seed=2)
 METRIC = "accepted tok/s, Qwen3-8B EAGLE3 k=5 bs64; verify-attn HBM GB/s % of peak"
@@ -318,7 +318,7 @@ def attention_only(args) -> None:
     copy_us = timed(lambda: dst.copy_(src), args.roofline_repeats)
     # a read-only reference (1 GiB read, 4 bytes written): the FETCH_SIZE
     # scale for a kernel that reads with wide vector loads and writes little
-    total = torch.empty(1, dtype=torch.float32, device=dev)
+    total = torch.empty((), dtype=torch.float32, device=dev)
     flat = src.view(torch.float32)
     read_us = timed(lambda: torch.sum(flat, 0, out=total), args.roofline_repeats)
     byts = sum(seqlens) * hkv * d * 2 * 2 + T * hq * d * 2 * 2
