@@ -93,6 +93,23 @@ inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 
 // caches early and do not displace lines that are still to be re-read.
 constexpr int kLoadStreamed = 2;
 
+// Streaming (non-temporal) stores for rows that no kernel re-reads soon
+// from a cache: new KV-cache rows (read next by the attention, from HBM)
+// and the fused kernel's query rows.  Each call site writes whole 128-byte
+// lines per instruction.  The scattered cache rows of the verify step
+// (6144 rows of 256 bytes at 64 KiB strides) otherwise linger dirty and
+// drain while the next kernel streams its reads: the verify attention that
+// follows the fused norm/RoPE/store launch took 59.3 us per call against
+// 58.2-58.5 us with these stores streamed (Qwen3-8B bench shapes, kernel
+// trace; 57.0-57.9 us with no store before it).
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void store_streamed(uint16_t* p, uint16_t v) {
+  __builtin_nontemporal_store(v, p);
+}
+__device__ __forceinline__ void store_streamed(uint4* p, uint4 v) {
+  __builtin_nontemporal_store(__builtin_bit_cast(u32x4_t, v), reinterpret_cast<u32x4_t*>(p));
+}
+
 // Raw buffer descriptor over num_records bytes at base: loads at offsets
 // past the end return zeros (dword 3: 32-bit data format, no swizzle).
 constexpr int kRsrcWord3 = 0x00020000;

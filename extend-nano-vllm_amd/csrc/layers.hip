@@ -244,9 +244,10 @@ __device__ __forceinline__ void put_cache_pair(void* cache, int64_t dst, int lan
     c[lane] = static_cast<uint8_t>(f32_to_e4m3(bf16_to_f32(a) / scale));
     c[lane + 64] = static_cast<uint8_t>(f32_to_e4m3(bf16_to_f32(b) / scale));
   } else {
+    // one full 128-byte line per instruction (64 lanes x 2 bytes)
     uint16_t* c = static_cast<uint16_t*>(cache) + dst;
-    c[lane] = a;
-    c[lane + 64] = b;
+    store_streamed(c + lane, a);
+    store_streamed(c + lane + 64, b);
   }
 }
 
@@ -297,8 +298,8 @@ qk_norm_rope_store_kernel(const uint16_t* __restrict__ qkv, int64_t row_stride,
   const uint16_t y2 = f32_to_bf16(x2 * c + x1 * s);
   if (is_q) {
     uint16_t* qd = q_out + (static_cast<int64_t>(t) * hq + head) * 128;
-    qd[lane] = y1;
-    qd[lane + 64] = y2;
+    store_streamed(qd + lane, y1);
+    store_streamed(qd + lane + 64, y2);
   } else {
     put_cache_pair<FP8>(k_cache, dst, lane, y1, y2, FP8 && k_scale_p ? *k_scale_p : 1.0f);
   }

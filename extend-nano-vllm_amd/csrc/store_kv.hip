@@ -50,8 +50,8 @@ store_kvcache_kernel(const uint16_t* __restrict__ key, int64_t key_row_stride,
       const uint4 kw = reinterpret_cast<const uint4*>(k)[i];
       const uint4 vw = reinterpret_cast<const uint4*>(v)[i];
       if constexpr (!FP8) {
-        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(k_cache) + dst) = kw;
-        *reinterpret_cast<uint4*>(static_cast<uint16_t*>(v_cache) + dst) = vw;
+        store_streamed(reinterpret_cast<uint4*>(static_cast<uint16_t*>(k_cache) + dst), kw);
+        store_streamed(reinterpret_cast<uint4*>(static_cast<uint16_t*>(v_cache) + dst), vw);
       } else {
         const uint32_t kin[4] = {kw.x, kw.y, kw.z, kw.w};
         const uint32_t vin[4] = {vw.x, vw.y, vw.z, vw.w};
