@@ -151,7 +151,7 @@ int nva_aux_gather(const void *const *hidden, const void *const *residual, int32
  *   q_i == 0 gets accept_len 0 and bonus -1.
  * workspace: nva_argmax_workspace_size(num_tokens, num_seqs, vocab) bytes,
  *   8-byte aligned, no initialisation needed (per-chunk partial maxima).
- * Two kernels are enqueued (chunk partials, then a per-sequence merge).
+ * Two kernels are enqueued (chunk partials, then the merge and accept scan).
  * ------------------------------------------------------------------- */
 size_t nva_argmax_workspace_size(int32_t num_rows, int32_t num_seqs, int32_t vocab);
 

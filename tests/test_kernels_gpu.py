@@ -158,17 +158,20 @@ def test_argmax_accept_graph_replay(K, cuda):
         torch.cuda.synchronize()
 
 
-@pytest.mark.parametrize("shape", ["many_chunks", "multi_pass"])
+@pytest.mark.parametrize("shape", ["many_chunks", "multi_pass", "wave_per_sequence"])
 def test_argmax_finalize_passes(K, cuda, shape):
-    """The finalize kernels load the chunk keys of as many rows as a wave's
-    lanes hold per pass: rows split into more than 64 chunks (one row per
-    pass, lane-strided keys), and sequences longer than one pass of several
-    rows with the accepted prefix running across pass boundaries."""
+    """Both merge kernels.  Up to 8192 chunk keys go through the one-workgroup
+    merge: rows split into more than 16 chunks, and long sequences with the
+    accepted prefix running far into them.  Beyond that (here 8400 keys) the
+    wave-per-sequence merge loads the keys of as many rows as a wave's lanes
+    hold per pass, with the accepted prefix running across pass boundaries."""
     g = torch.Generator().manual_seed(21)
     if shape == "many_chunks":
-        qs, vocab = [3, 1], 300000            # > 64 chunks of >= 4096 elements per row
-    else:
-        qs, vocab = [30, 27, 9, 30], 32768    # eight chunks per row: eight rows per pass
+        qs, vocab = [3, 1], 300000            # 19 chunks of 16384 elements per row
+    elif shape == "multi_pass":
+        qs, vocab = [30, 27, 9, 30], 32768    # two chunks per row
+    else:                                     # 840 rows x 10 chunks: past the one-workgroup limit
+        qs, vocab = [30, 27, 9, 30] + [6] * 124, 151936
     t = sum(qs)
     logits = torch.randn(t, vocab, generator=g).to(torch.bfloat16)
     cu = torch.tensor([0] + np.cumsum(qs).tolist(), dtype=torch.int32)
@@ -176,7 +179,7 @@ def test_argmax_finalize_passes(K, cuda, shape):
     np.testing.assert_array_equal(ref_am, logits.argmax(-1).numpy())
     ids = torch.randint(0, vocab, (t,), generator=g)
     # accept every proposal up to a per-sequence row, then reject
-    stops = [2, 0, 8, 29][: len(qs)]
+    stops = ([2, 0, 8, 29] + [i % 6 for i in range(len(qs))])[: len(qs)]
     for i, q in enumerate(qs):
         s = int(cu[i])
         for j in range(min(stops[i], q - 1)):
@@ -799,8 +802,9 @@ def _picks(c, count, seed):
 def test_full_size_verify_matches_oracle_on_sampled_sequences(K, cuda, name):
     """At the BASELINE configs' full sizes the whole batch runs on the GPU in
     one launch (config 4: FP8 pages, stream ranges over 128 sequences of
-    4096-16384 keys; config 5: 64-row tiles, 3072-key splits and the
-    combine, the first 30% of every sequence's blocks shared), and the
+    4096-16384 keys; config 5: 64-row tiles, splits of three quarters of
+    the longest sequence (6144 keys) and the combine, the first 30% of
+    every sequence's blocks shared), and the
     rows of 8 sampled sequences -- the longest and the shortest among them
     -- are held to the CPU oracle on the same pages: the textbook attention
     within 2e-2 (the north star's bound) and, for FP8, the restated
@@ -818,8 +822,8 @@ def test_full_size_verify_matches_oracle_on_sampled_sequences(K, cuda, name):
     torch.cuda.synchronize()
     picks = _picks(c, 8, seed=5)
     if not fp8:
-        # config 5: at least one sampled sequence needs three splits
-        assert max(c["lens"][i] for i in picks) > 2 * 3072
+        # config 5: at least one sampled sequence is split (and combined)
+        assert max(c["lens"][i] for i in picks) > 6144
     kb, vb, sub_bt, rows, qb, lens = _sample_rows(c, picks)
     q_len = c["q_len"]
     cu = np.arange(0, len(picks) * q_len + 1, q_len, dtype=np.int32)
