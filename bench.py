@@ -13,8 +13,10 @@ The same JSON line carries
                  step of the same workload runs its verify forward eagerly
                  (the timed steps replay HIP graphs, inside which ROCm torch
                  cannot record timing events), and its 36 verify-attention
-                 launches are re-issued back to back --roofline-repeats times
-                 between two events; achieved = algorithmic bytes per launch /
+                 launches, --roofline-repeats times over, are captured in a
+                 HIP graph whose replay is timed between two events (so the
+                 host's launch rate cannot pace them); achieved = algorithmic
+                 bytes per launch /
                  mean launch time, algorithmic bytes = sum_i L_i*Hkv*D*2B*2
                  (K and V read once) + T*Hq*D*2B*2 (Q in, O out);
   cpu_baseline:  the reference's host acceptance logic (per-sequence bf16
@@ -72,7 +74,8 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--roofline-repeats", type=int, default=10,
                     help="times the verify-attention launches of one step are re-issued "
-                         "between HIP events for the roofline figure")
+                         "(captured in one HIP graph, replayed between HIP events) for the "
+                         "roofline figure")
     ap.add_argument("--reference-steps", type=int, default=5,
                     help="steps timed with the reference's step structure for comparison, on "
                          "this build's kernels and on torch attention (0 to skip)")
@@ -116,11 +119,11 @@ class AttnTimer:
     While ``capture`` is set, every verify-attention call made by the verify
     forward (launched eagerly) is recorded with its arguments and its
     algorithmic bytes, computed from the host-side metadata.  ``measure``
-    then re-issues those exact launches back to back, ``repeats`` times, on
-    the current stream (the one the kernels are enqueued on), between two HIP
-    events, so that the mean launch time is the kernels' own time and not the
-    host's launch latency.  The re-issued launches only read the K/V cache
-    and write fresh output buffers."""
+    then captures those exact launches, ``repeats`` times over, in a HIP
+    graph and times one replay on the current stream (the one the kernels
+    are enqueued on) between two HIP events, so that the mean launch time is
+    the kernels' own time and not the host's launch rate.  The re-issued
+    launches only read the K/V cache and write fresh output buffers."""
 
     def __init__(self):
         self.capture = False
@@ -160,15 +163,25 @@ class AttnTimer:
         for args in self.calls:  # warm the workspace cache
             self.orig(*args)
         torch.cuda.synchronize()
+        # the launches are captured in a HIP graph and one replay is timed,
+        # so that the host's launch rate (the Python wrapper per call) cannot
+        # pace the kernels: eager re-issue read 66.7 us per call on a box
+        # whose trace showed 58 us of kernel time
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(repeats):
+                for args in self.calls:
+                    self.orig(*args)
+        graph.replay()
+        torch.cuda.synchronize()
         stream = torch.cuda.current_stream()
         s = torch.cuda.Event(enable_timing=True)
         e = torch.cuda.Event(enable_timing=True)
         s.record(stream)
-        for _ in range(repeats):
-            for args in self.calls:
-                self.orig(*args)
+        graph.replay()
         e.record(stream)
         torch.cuda.synchronize()
+        del graph
         launches = repeats * len(self.calls)
         mean_ms = s.elapsed_time(e) / launches
         mean_bytes = sum(self.bytes) / len(self.bytes)
