@@ -360,11 +360,16 @@ argmax_rows_finalize_kernel(const uint64_t* __restrict__ partials, int32_t chunk
   const int32_t rn = num_rows - r0 < per_pass ? num_rows - r0 : per_pass;
   int32_t my_row;
   const uint64_t mine = pass_keys(partials, chunks, r0, rn, my_row);
+  // lane j keeps row j's index, so the index-map lookups of the pass are
+  // one vector load (one memory latency) and the stores one vector store
+  const int lane = wave_lane();
+  uint32_t row_idx = 0;
   for (int32_t j = 0; j < rn; ++j) {
     const uint64_t k = wave_max(my_row == j ? mine : 0);
-    const uint32_t idx = 0xFFFFFFFFu - static_cast<uint32_t>(k);
-    if (wave_lane() == 0) out64[r0 + j] = static_cast<int64_t>(idx) + (index_map ? index_map[idx] : 0);
+    if (lane == j) row_idx = 0xFFFFFFFFu - static_cast<uint32_t>(k);
   }
+  if (lane < rn)
+    out64[r0 + lane] = static_cast<int64_t>(row_idx) + (index_map ? index_map[row_idx] : 0);
 }
 
 // Chunks of kChunkElems elements per row.
