@@ -7,6 +7,15 @@
 // every thread derives the positions and slots of a strided set of tokens
 // (sequence found by binary search over the scanned offsets).  The work is
 // a few thousand integers; the point is removing host work, not bandwidth.
+//
+// The commit form derives the same metadata for the draft's replay of the
+// committed tails (model_runner.py:1216-1249, the per-token contexts of
+// :1127-1156): sequence i commits accept_len[i] + 1 rows (its accepted
+// drafts, then the bonus token) taken from its verify rows i * q_stride ..,
+// so the query lengths come from the accept scan's output on the device,
+// and each commit row also gets its verify row, its token (the verify
+// argmax of that row, which an accepted draft equals) and each sequence its
+// last commit row, whose draft states seed the next proposal.
 #include "common.h"
 
 namespace nva {
@@ -31,13 +40,26 @@ __device__ int block_scan(int v, int* sh) {
   return r;
 }
 
+// Commit-form inputs and outputs (unused by the verify form).
+struct CommitArgs {
+  int32_t q_stride;                 // verify rows per sequence
+  const int32_t* verify_argmax;     // [num_verify_rows]
+  int32_t num_verify_rows;
+  int32_t* verify_rows;             // [num_tokens]
+  int64_t* token_ids;               // [num_tokens]
+  int64_t* last_rows;               // [num_seqs]
+};
+
+// COMMIT: q_lens holds accept lengths; sequence i has min(max(a_i, 0) + 1,
+// q_stride) rows.
+template <bool COMMIT>
 __global__ void __launch_bounds__(kMetaThreads)
 verify_metadata_kernel(const int32_t* __restrict__ start_pos, const int32_t* __restrict__ q_lens,
                        int32_t num_seqs, const int32_t* __restrict__ block_tables,
                        int64_t bt_stride, int32_t max_blocks, int32_t block_size,
                        int32_t* __restrict__ cu_q_out, int32_t* __restrict__ cu_k_out,
                        int64_t* __restrict__ positions, int32_t* __restrict__ slots,
-                       int32_t num_tokens) {
+                       int32_t num_tokens, CommitArgs ca) {
   __shared__ int cu_q[kMaxMetaSeqs + 1];
   __shared__ int cu_k[kMaxMetaSeqs + 1];
   __shared__ int scan[kMetaThreads];
@@ -49,7 +71,11 @@ verify_metadata_kernel(const int32_t* __restrict__ start_pos, const int32_t* __r
   int carry_q = 0, carry_k = 0;
   for (int base = 0; base < num_seqs; base += kMetaThreads) {
     const int i = base + tid;
-    const int q = i < num_seqs ? q_lens[i] : 0;
+    int q = i < num_seqs ? q_lens[i] : 0;
+    if (COMMIT && i < num_seqs) {
+      q = (q < 0 ? 0 : q) + 1;
+      q = q < ca.q_stride ? q : ca.q_stride;
+    }
     const int k = i < num_seqs ? start_pos[i] + q : 0;
     const int iq = block_scan(q, scan) + carry_q;
     const int ik = block_scan(k, scan) + carry_k;
@@ -66,11 +92,13 @@ verify_metadata_kernel(const int32_t* __restrict__ start_pos, const int32_t* __r
   for (int i = tid; i <= num_seqs; i += kMetaThreads) {
     cu_q_out[i] = cu_q[i];
     cu_k_out[i] = cu_k[i];
+    if (COMMIT && i < num_seqs) ca.last_rows[i] = static_cast<int64_t>(cu_q[i + 1]) - 1;
   }
   const int total = cu_q[num_seqs];
   for (int t = tid; t < num_tokens; t += kMetaThreads) {
     int64_t pos = 0;
     int32_t slot = -1;
+    int32_t vrow = -1;
     if (t < total) {
       // sequence s with cu_q[s] <= t < cu_q[s + 1] (empty sequences skipped)
       int lo = 0, hi = num_seqs;
@@ -85,9 +113,16 @@ verify_metadata_kernel(const int32_t* __restrict__ start_pos, const int32_t* __r
         const int32_t id = block_tables[static_cast<int64_t>(lo) * bt_stride + b];
         if (id >= 0) slot = id * block_size + p % block_size;
       }
+      if (COMMIT) vrow = lo * ca.q_stride + (t - cu_q[lo]);
     }
     positions[t] = pos;
     slots[t] = slot;
+    if (COMMIT) {
+      // rows past the committed ones read verify row 0 (never attended)
+      const int32_t src = vrow >= 0 && vrow < ca.num_verify_rows ? vrow : 0;
+      ca.verify_rows[t] = vrow;
+      ca.token_ids[t] = ca.num_verify_rows > 0 ? ca.verify_argmax[src] : 0;
+    }
   }
 }
 
@@ -109,8 +144,36 @@ extern "C" int nva_verify_metadata(const int32_t* start_pos, const int32_t* q_le
     return NVA_ERR_ARG;
   if (num_seqs > 0 && (!start_pos || !q_lens || (max_blocks_per_seq > 0 && !block_tables)))
     return NVA_ERR_ARG;
-  verify_metadata_kernel<<<1, kMetaThreads, 0, static_cast<hipStream_t>(stream)>>>(
+  verify_metadata_kernel<false><<<1, kMetaThreads, 0, static_cast<hipStream_t>(stream)>>>(
       start_pos, q_lens, num_seqs, block_tables, block_table_stride, max_blocks_per_seq, block_size,
-      cu_seqlens_q, cu_seqlens_k, positions, slot_mapping, num_tokens);
+      cu_seqlens_q, cu_seqlens_k, positions, slot_mapping, num_tokens, CommitArgs{});
+  return launch_status();
+}
+
+extern "C" int nva_commit_metadata(const int32_t* start_pos, const int32_t* accept_len,
+                                   int32_t num_seqs, int32_t q_stride,
+                                   const int32_t* verify_argmax, int32_t num_verify_rows,
+                                   const int32_t* block_tables, int64_t block_table_stride,
+                                   int32_t max_blocks_per_seq, int32_t block_size,
+                                   int32_t* cu_seqlens_q, int32_t* cu_seqlens_k,
+                                   int64_t* positions, int32_t* slot_mapping,
+                                   int32_t* verify_rows, int64_t* token_ids, int64_t* last_rows,
+                                   int32_t num_tokens, void* stream) {
+  if (num_seqs < 0 || num_tokens < 0 || block_size <= 0 || max_blocks_per_seq < 0 ||
+      q_stride <= 0 || num_verify_rows < 0)
+    return NVA_ERR_ARG;
+  if (num_seqs > kMaxMetaSeqs) return NVA_ERR_UNSUPPORTED;
+  if (block_table_stride < max_blocks_per_seq) return NVA_ERR_ARG;
+  if (!cu_seqlens_q || !cu_seqlens_k) return NVA_ERR_ARG;
+  if (num_tokens > 0 && (!positions || !slot_mapping || !verify_rows || !token_ids))
+    return NVA_ERR_ARG;
+  if (num_tokens > 0 && num_verify_rows > 0 && !verify_argmax) return NVA_ERR_ARG;
+  if (num_seqs > 0 && (!start_pos || !accept_len || !last_rows ||
+                       (max_blocks_per_seq > 0 && !block_tables)))
+    return NVA_ERR_ARG;
+  const CommitArgs ca{q_stride, verify_argmax, num_verify_rows, verify_rows, token_ids, last_rows};
+  verify_metadata_kernel<true><<<1, kMetaThreads, 0, static_cast<hipStream_t>(stream)>>>(
+      start_pos, accept_len, num_seqs, block_tables, block_table_stride, max_blocks_per_seq,
+      block_size, cu_seqlens_q, cu_seqlens_k, positions, slot_mapping, num_tokens, ca);
   return launch_status();
 }

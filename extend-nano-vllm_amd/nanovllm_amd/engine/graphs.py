@@ -322,11 +322,13 @@ class DeviceCommitGraph(_GraphBase):
         self.i64 = _Staging({"state": self.bs}, torch.int64, dev)
         self.i64.fill("state", [runner.scratch_state_row] * self.bs)
         self.i64.upload()
-        self.t_idx = torch.arange(self.T, dtype=torch.int64, device=dev)
         self.cu_q = torch.zeros(self.bs + 1, dtype=torch.int32, device=dev)
         self.cu_k = torch.zeros(self.bs + 1, dtype=torch.int32, device=dev)
         self.pos = torch.zeros(self.T, dtype=torch.int64, device=dev)
         self.slots = torch.zeros(self.T, dtype=torch.int32, device=dev)
+        self.rows = torch.zeros(self.T, dtype=torch.int32, device=dev)
+        self.ids = torch.zeros(self.T, dtype=torch.int64, device=dev)
+        self.last = torch.zeros(self.bs, dtype=torch.int64, device=dev)
         self._capture(self._body)
 
     def _body(self):
@@ -336,25 +338,19 @@ class DeviceCommitGraph(_GraphBase):
         bs, q, T = self.bs, self.q, self.T
         bt = v.i32.dev_view("bt").view(bs, v.max_blocks)
         start = v.i32.dev_view("start")
-        qlen = v.out[T:T + bs] + 1
-        K.verify_metadata(start, qlen, bt, r.block_size, T, self.cu_q, self.cu_k, self.pos,
-                          self.slots)
-        cu = self.cu_q.long()
-        seq = torch.searchsorted(cu[1:], self.t_idx, right=True)
-        seq_c = seq.clamp(max=bs - 1)
-        rows = seq_c * q + (self.t_idx - cu.index_select(0, seq_c))
-        rows = torch.where(seq < bs, rows, torch.full_like(rows, -1))
-        ids = v.out.index_select(0, rows.clamp(min=0)).long()
-        combined = draft.combine_hidden_states(aux_concat(v.aux, rows.to(torch.int32)))
+        # one launch: the commit rows' positions, slots, verify rows and
+        # tokens, and each sequence's last commit row, from the accept scan
+        K.commit_metadata(start, v.out[T:T + bs], q, v.out[:T], bt, r.block_size, T, self.cu_q,
+                          self.cu_k, self.pos, self.slots, self.rows, self.ids, self.last)
+        combined = draft.combine_hidden_states(aux_concat(v.aux, self.rows))
         set_context(True, self.cu_q, self.cu_k, q, r.max_seqlen_k, self.slots, None, bt)
         try:
-            hidden, feedback = draft.forward_with_cache(ids, self.pos, combined)
+            hidden, feedback = draft.forward_with_cache(self.ids, self.pos, combined)
         finally:
             reset_context()
-        last = cu[1:] - 1
         state = self.i64.dev_view("state")
-        r.state_hidden.index_copy_(0, state, hidden.index_select(0, last))
-        r.state_feedback.index_copy_(0, state, feedback.index_select(0, last))
+        r.state_hidden.index_copy_(0, state, hidden.index_select(0, self.last))
+        r.state_feedback.index_copy_(0, state, feedback.index_select(0, self.last))
 
     def run(self, state_rows) -> None:
         """state_rows: the draft-state row of each sequence of the verify

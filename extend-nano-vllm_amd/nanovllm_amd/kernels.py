@@ -675,3 +675,50 @@ def verify_metadata(start_pos: torch.Tensor, q_lens: torch.Tensor, block_tables:
                                   cu_seqlens_k.data_ptr(), positions.data_ptr(),
                                   slot_mapping.data_ptr(), int(num_tokens), _stream()),
           "verify_metadata")
+
+
+def commit_metadata(start_pos: torch.Tensor, accept_len: torch.Tensor, q_stride: int,
+                    verify_argmax: torch.Tensor, block_tables: torch.Tensor, block_size: int,
+                    num_tokens: int, cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor,
+                    positions: torch.Tensor, slot_mapping: torch.Tensor,
+                    verify_rows: torch.Tensor, token_ids: torch.Tensor,
+                    last_rows: torch.Tensor) -> None:
+    """Device-side metadata of the draft's replay of the committed tails
+    (commit_eagle3, model_runner.py:1216-1249): sequence i commits
+    accept_len[i] + 1 rows (at most q_stride) starting at position
+    start_pos[i], taken from its verify rows i * q_stride ..  Writes
+    verify_metadata's outputs for those lengths, plus per commit row its
+    verify row (int32, -1 past the committed rows) and its token (the verify
+    argmax of that row, int64), and per sequence its last commit row
+    (int64)."""
+    lib = _native.load()
+    _require_cuda(start_pos, accept_len, verify_argmax, block_tables, cu_seqlens_q, cu_seqlens_k,
+                  positions, slot_mapping, verify_rows, token_ids, last_rows)
+    b = start_pos.numel()
+    for t, name in ((start_pos, "start_pos"), (accept_len, "accept_len"),
+                    (verify_argmax, "verify_argmax"), (cu_seqlens_q, "cu_seqlens_q"),
+                    (cu_seqlens_k, "cu_seqlens_k"), (slot_mapping, "slot_mapping"),
+                    (verify_rows, "verify_rows")):
+        _i32(t, name)
+    if accept_len.numel() != b or cu_seqlens_q.numel() < b + 1 or cu_seqlens_k.numel() < b + 1 \
+            or last_rows.numel() < b:
+        raise ValueError("start_pos / accept_len / cu_seqlens / last_rows sizes do not match")
+    for t, name in ((positions, "positions"), (token_ids, "token_ids"), (last_rows, "last_rows")):
+        if t.dtype != torch.int64 or not t.is_contiguous():
+            raise TypeError(f"{name} must be contiguous int64")
+    if positions.numel() < num_tokens or slot_mapping.numel() < num_tokens or \
+            verify_rows.numel() < num_tokens or token_ids.numel() < num_tokens:
+        raise ValueError("positions / slot_mapping / verify_rows / token_ids need num_tokens "
+                         "entries")
+    if block_tables.dtype != torch.int32 or block_tables.dim() != 2 or block_tables.stride(1) != 1 \
+            or block_tables.shape[0] < b:
+        raise TypeError("block_tables must be int32 [num_seqs, max_blocks]")
+    check(lib.nva_commit_metadata(start_pos.data_ptr(), accept_len.data_ptr(), b, int(q_stride),
+                                  verify_argmax.data_ptr(), verify_argmax.numel(),
+                                  block_tables.data_ptr(), block_tables.stride(0),
+                                  block_tables.shape[1], int(block_size), cu_seqlens_q.data_ptr(),
+                                  cu_seqlens_k.data_ptr(), positions.data_ptr(),
+                                  slot_mapping.data_ptr(), verify_rows.data_ptr(),
+                                  token_ids.data_ptr(), last_rows.data_ptr(), int(num_tokens),
+                                  _stream()),
+          "commit_metadata")

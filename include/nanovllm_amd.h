@@ -359,6 +359,35 @@ int nva_verify_metadata(const int32_t *start_pos, const int32_t *q_lens, int32_t
                         int32_t *cu_seqlens_k, int64_t *positions, int32_t *slot_mapping,
                         int32_t num_tokens, void *stream);
 
+/* ---------------------------------------------------------------------
+ * Commit metadata: the draft's replay of the committed tails, derived on
+ * the device from the accept scan's results.
+ * Replaces what commit_eagle3 builds per sequence on the host -- the
+ *   output token ids, their positions, the verify rows whose aux states
+ *   feed the fc, the per-token paged contexts and the last row that seeds
+ *   the draft state (nanovllm/engine/model_runner.py:1216-1249, contexts
+ *   :1127-1156) -- for a whole verify batch at once.
+ * Sequence i commits q_i = min(max(accept_len[i], 0) + 1, q_stride) rows
+ *   (its accepted drafts, then the bonus token) from its verify rows
+ *   i * q_stride .. i * q_stride + q_i - 1; cu_seqlens_q / cu_seqlens_k /
+ *   positions / slot_mapping are nva_verify_metadata's outputs for
+ *   (start_pos, q_i).  Per commit row t of sequence i:
+ *   verify_rows[t] = i * q_stride + (t - cu_seqlens_q[i]);
+ *   token_ids[t] = verify_argmax[verify_rows[t]] (int64; an accepted draft
+ *   equals the argmax of its row);
+ *   rows t >= cu_seqlens_q[num_seqs] get verify row -1, token
+ *   verify_argmax[0], position 0 and slot -1.
+ * last_rows[i] = cu_seqlens_q[i+1] - 1 (int64).  num_seqs <= 2048; every
+ *   array is device memory.
+ * ------------------------------------------------------------------- */
+int nva_commit_metadata(const int32_t *start_pos, const int32_t *accept_len, int32_t num_seqs,
+                        int32_t q_stride, const int32_t *verify_argmax, int32_t num_verify_rows,
+                        const int32_t *block_tables, int64_t block_table_stride,
+                        int32_t max_blocks_per_seq, int32_t block_size, int32_t *cu_seqlens_q,
+                        int32_t *cu_seqlens_k, int64_t *positions, int32_t *slot_mapping,
+                        int32_t *verify_rows, int64_t *token_ids, int64_t *last_rows,
+                        int32_t num_tokens, void *stream);
+
 /* SiluAndMul (nanovllm/layers/activation.py:11-14): x rows [a | b] of
  *   2*intermediate elements -> out = bf16(bf16(silu(a)) * b). */
 int nva_silu_mul(const void *x, int64_t x_row_stride, void *out, int64_t out_row_stride,

@@ -296,3 +296,29 @@ def verify_metadata(start_pos, q_lens, block_tables, block_size, num_tokens):
     slots += [-1] * pad
     return (np.array(cu_q, np.int32), np.array(cu_k, np.int32),
             np.array(positions[:num_tokens], np.int64), np.array(slots[:num_tokens], np.int32))
+
+
+def commit_metadata(start_pos, accept_len, q_stride, verify_argmax, block_tables, block_size,
+                    num_tokens):
+    """Restates what commit_eagle3 builds for one sequence
+    (nanovllm/engine/model_runner.py:1216-1249: the output tokens, their
+    positions start .. start + n - 1, the first n aux rows of the
+    sequence's verify block, the last row's draft state), laid end to end
+    for a batch: sequence i commits n_i = min(max(a_i, 0) + 1, q_stride)
+    tokens, the verify argmax of its rows i * q_stride .. + n_i - 1 (the
+    accepted drafts equal the argmax of their rows; the last is the
+    bonus).  Rows past the committed ones read verify row -1 -> token of
+    row 0.  Returns (cu_q, cu_k, positions, slots, verify_rows, token_ids,
+    last_rows) as numpy arrays."""
+    n = [min(max(int(a), 0) + 1, int(q_stride)) for a in accept_len]
+    cu_q, cu_k, positions, slots = verify_metadata(start_pos, n, block_tables, block_size,
+                                                   num_tokens)
+    rows = []
+    for i, ni in enumerate(n):
+        rows += [i * int(q_stride) + j for j in range(ni)]
+    rows = (rows + [-1] * num_tokens)[:num_tokens]
+    am = np.asarray(verify_argmax)
+    ids = [int(am[r]) if 0 <= r < len(am) else (int(am[0]) if len(am) else 0) for r in rows]
+    last = [int(cu_q[i + 1]) - 1 for i in range(len(n))]
+    return (cu_q, cu_k, positions, slots, np.array(rows, np.int32), np.array(ids, np.int64),
+            np.array(last, np.int64))

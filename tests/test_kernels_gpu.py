@@ -511,6 +511,40 @@ def test_verify_metadata_matches_oracle(K, cuda, num_seqs, seed):
     np.testing.assert_array_equal(o_slots.cpu().numpy(), slots)
 
 
+@pytest.mark.parametrize("num_seqs,q_stride,seed", [(1, 6, 0), (64, 6, 1), (300, 8, 2), (5, 1, 3)])
+def test_commit_metadata_matches_oracle(K, cuda, num_seqs, q_stride, seed):
+    """Device metadata of the draft's replay of the committed tails:
+    bit-exact against the restatement, from accept lengths taken straight
+    from an accept-scan-shaped buffer (including out-of-range ones, which
+    clamp), with -1 block ids, page crossings and padding rows."""
+    g = np.random.default_rng(seed)
+    bs, width = 256, 12
+    accept = g.integers(0, q_stride, num_seqs).astype(np.int32)
+    accept[g.random(num_seqs) < 0.05] = q_stride + 3
+    accept[g.random(num_seqs) < 0.05] = -2
+    start = g.integers(0, bs * (width - 1) - 16, num_seqs).astype(np.int32)
+    tables = g.integers(0, 5000, (num_seqs, width)).astype(np.int32)
+    tables[g.random((num_seqs, width)) < 0.05] = -1
+    t = num_seqs * q_stride
+    argmax = g.integers(0, 151936, t).astype(np.int32)
+    ref = oracle.commit_metadata(start, accept, q_stride, argmax, tables, bs, t)
+    d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
+    # the engine passes slices of the accept scan's one int32 buffer
+    out = d(np.concatenate([argmax, accept, np.full(num_seqs, -9, np.int32)]))
+    o_cu_q = torch.full((num_seqs + 1,), -7, dtype=torch.int32, device=cuda)
+    o_cu_k = torch.full((num_seqs + 1,), -7, dtype=torch.int32, device=cuda)
+    o_pos = torch.full((t,), -7, dtype=torch.int64, device=cuda)
+    o_slots = torch.full((t,), -7, dtype=torch.int32, device=cuda)
+    o_rows = torch.full((t,), -7, dtype=torch.int32, device=cuda)
+    o_ids = torch.full((t,), -7, dtype=torch.int64, device=cuda)
+    o_last = torch.full((num_seqs,), -7, dtype=torch.int64, device=cuda)
+    K.commit_metadata(d(start), out[t:t + num_seqs], q_stride, out[:t], d(tables), bs, t,
+                      o_cu_q, o_cu_k, o_pos, o_slots, o_rows, o_ids, o_last)
+    torch.cuda.synchronize()
+    for got, want in zip((o_cu_q, o_cu_k, o_pos, o_slots, o_rows, o_ids, o_last), ref):
+        np.testing.assert_array_equal(got.cpu().numpy(), want)
+
+
 # ---------------------------------------------------------------- layer kernels + fused K2
 
 def _qk_norm_rope_reference(qkv, positions, qw, kw, cos_sin, hq, hkv, d, eps):

@@ -344,6 +344,58 @@ def test_verify_metadata_agrees_with_engine_host_path(monkeypatch):
         reset_context()
 
 
+def test_commit_metadata_hand_worked():
+    # two sequences of a q = 3 verify batch accept 1 and 2 drafts: sequence 0
+    # commits verify rows 0, 1 at positions 10, 11 (physical block 7);
+    # sequence 1 commits rows 3, 4, 5 at positions 255 .. 257, crossing from
+    # physical block 4 into physical block 9; one padding row follows
+    am = [100, 101, 102, 103, 104, 105]
+    cu_q, cu_k, pos, slots, rows, ids, last = oracle.commit_metadata(
+        [10, 255], [1, 2], 3, am, [[7, 8], [4, 9]], 256, 6)
+    assert cu_q.tolist() == [0, 2, 5] and cu_k.tolist() == [0, 12, 270]
+    assert pos.tolist() == [10, 11, 255, 256, 257, 0]
+    assert slots.tolist() == [7 * 256 + 10, 7 * 256 + 11, 4 * 256 + 255, 9 * 256, 9 * 256 + 1, -1]
+    assert rows.tolist() == [0, 1, 3, 4, 5, -1]
+    assert ids.tolist() == [100, 101, 103, 104, 105, 100]
+    assert last.tolist() == [1, 4]
+    # accept lengths outside [0, q - 1] are clamped to one and to q rows
+    cu_q, _, _, _, rows, _, last = oracle.commit_metadata([0, 0], [-4, 9], 3, am, [[1], [2]],
+                                                          256, 6)
+    assert cu_q.tolist() == [0, 1, 4] and rows.tolist() == [0, 3, 4, 5, -1, -1]
+    assert last.tolist() == [0, 3]
+
+
+def test_commit_metadata_agrees_with_torch_gather_formulation():
+    """The rows, tokens and last rows as a torch searchsorted / where /
+    index_select chain over the verify batch (an independent formulation)
+    equal the restatement's, on random accept lengths."""
+    import random
+
+    rng = random.Random(9)
+    for trial in range(20):
+        bs, q = rng.randrange(1, 12), rng.randrange(1, 9)
+        t = bs * q
+        accept = [rng.randrange(0, q) for _ in range(bs)]
+        starts = [rng.randrange(0, 700) for _ in range(bs)]
+        tables = [rng.sample(range(50), 4) for _ in range(bs)]
+        am = [rng.randrange(0, 1000) for _ in range(t)]
+        cu_q, _, pos, _, rows, ids, last = oracle.commit_metadata(starts, accept, q, am, tables,
+                                                                  256, t)
+        cu = torch.tensor([0] + np.cumsum([a + 1 for a in accept]).tolist())
+        t_idx = torch.arange(t)
+        seq = torch.searchsorted(cu[1:], t_idx, right=True)
+        seq_c = seq.clamp(max=bs - 1)
+        trows = seq_c * q + (t_idx - cu.index_select(0, seq_c))
+        trows = torch.where(seq < bs, trows, torch.full_like(trows, -1))
+        tids = torch.tensor(am).index_select(0, trows.clamp(min=0))
+        assert cu_q.tolist() == cu.tolist(), trial
+        assert rows.tolist() == trows.tolist(), trial
+        assert ids.tolist() == tids.tolist(), trial
+        assert last.tolist() == (cu[1:] - 1).tolist(), trial
+        committed = [s + j for s, a in zip(starts, accept) for j in range(a + 1)]
+        assert pos.tolist()[:len(committed)] == committed
+
+
 # ---------------------------------------------------------------- EAGLE3 draft step
 
 def _draft_weights(seed=0, h=256, hq=4, hkv=2, d=128, inter=512, vocab=300, nbr=True):
