@@ -68,6 +68,9 @@ verify_metadata_kernel(const int32_t* __restrict__ start_pos, const int32_t* __r
     cu_q[0] = 0;
     cu_k[0] = 0;
   }
+  // every thread reads cu_q[0] below, also when there is no sequence (and
+  // so no barrier inside the scan loop)
+  __syncthreads();
   int carry_q = 0, carry_k = 0;
   for (int base = 0; base < num_seqs; base += kMetaThreads) {
     const int i = base + tid;

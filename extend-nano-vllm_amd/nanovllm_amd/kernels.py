@@ -645,6 +645,17 @@ def silu_mul(x: torch.Tensor) -> torch.Tensor:
 
 # ---------------------------------------------------------------- verify metadata
 
+def _block_table_args(block_tables: torch.Tensor, num_seqs: int):
+    """(pointer, row stride, width) of an int32 [num_seqs, max_blocks] block
+    table; with no sequence nothing is read, so no table is needed."""
+    if num_seqs == 0:
+        return None, 0, 0
+    if block_tables.dtype != torch.int32 or block_tables.dim() != 2 or block_tables.stride(1) != 1 \
+            or block_tables.shape[0] < num_seqs:
+        raise TypeError("block_tables must be int32 [num_seqs, max_blocks]")
+    return block_tables.data_ptr(), block_tables.stride(0), block_tables.shape[1]
+
+
 def verify_metadata(start_pos: torch.Tensor, q_lens: torch.Tensor, block_tables: torch.Tensor,
                     block_size: int, num_tokens: int, cu_seqlens_q: torch.Tensor,
                     cu_seqlens_k: torch.Tensor, positions: torch.Tensor,
@@ -666,12 +677,10 @@ def verify_metadata(start_pos: torch.Tensor, q_lens: torch.Tensor, block_tables:
     if positions.dtype != torch.int64 or positions.numel() < num_tokens or \
             slot_mapping.numel() < num_tokens:
         raise ValueError("positions (int64) and slot_mapping need num_tokens entries")
-    if block_tables.dtype != torch.int32 or block_tables.dim() != 2 or block_tables.stride(1) != 1 \
-            or block_tables.shape[0] < b:
-        raise TypeError("block_tables must be int32 [num_seqs, max_blocks]")
+    bt_ptr, bt_stride, bt_width = _block_table_args(block_tables, b)
     check(lib.nva_verify_metadata(start_pos.data_ptr(), q_lens.data_ptr(), b,
-                                  block_tables.data_ptr(), block_tables.stride(0),
-                                  block_tables.shape[1], int(block_size), cu_seqlens_q.data_ptr(),
+                                  bt_ptr, bt_stride, bt_width, int(block_size),
+                                  cu_seqlens_q.data_ptr(),
                                   cu_seqlens_k.data_ptr(), positions.data_ptr(),
                                   slot_mapping.data_ptr(), int(num_tokens), _stream()),
           "verify_metadata")
@@ -710,13 +719,11 @@ def commit_metadata(start_pos: torch.Tensor, accept_len: torch.Tensor, q_stride:
             verify_rows.numel() < num_tokens or token_ids.numel() < num_tokens:
         raise ValueError("positions / slot_mapping / verify_rows / token_ids need num_tokens "
                          "entries")
-    if block_tables.dtype != torch.int32 or block_tables.dim() != 2 or block_tables.stride(1) != 1 \
-            or block_tables.shape[0] < b:
-        raise TypeError("block_tables must be int32 [num_seqs, max_blocks]")
+    bt_ptr, bt_stride, bt_width = _block_table_args(block_tables, b)
     check(lib.nva_commit_metadata(start_pos.data_ptr(), accept_len.data_ptr(), b, int(q_stride),
                                   verify_argmax.data_ptr(), verify_argmax.numel(),
-                                  block_tables.data_ptr(), block_tables.stride(0),
-                                  block_tables.shape[1], int(block_size), cu_seqlens_q.data_ptr(),
+                                  bt_ptr, bt_stride, bt_width, int(block_size),
+                                  cu_seqlens_q.data_ptr(),
                                   cu_seqlens_k.data_ptr(), positions.data_ptr(),
                                   slot_mapping.data_ptr(), verify_rows.data_ptr(),
                                   token_ids.data_ptr(), last_rows.data_ptr(), int(num_tokens),

@@ -484,11 +484,12 @@ def test_attention_skips_invalid_block_ids(K, cuda):
 
 # ---------------------------------------------------------------- verify metadata
 
-@pytest.mark.parametrize("num_seqs,seed", [(1, 0), (64, 1), (300, 2)])
+@pytest.mark.parametrize("num_seqs,seed", [(1, 0), (64, 1), (300, 2), (0, 3)])
 def test_verify_metadata_matches_oracle(K, cuda, num_seqs, seed):
     """Device prepare_prefill for verify rows: bit-exact against the
     restatement, with empty sequences, -1 block ids, page crossings and
-    padding rows (300 sequences exercise the multi-pass scan)."""
+    padding rows (300 sequences exercise the multi-pass scan; no sequence
+    at all leaves only padding rows)."""
     g = np.random.default_rng(seed)
     bs, width = 256, 12
     q = g.integers(0, 8, num_seqs).astype(np.int32)
@@ -511,7 +512,8 @@ def test_verify_metadata_matches_oracle(K, cuda, num_seqs, seed):
     np.testing.assert_array_equal(o_slots.cpu().numpy(), slots)
 
 
-@pytest.mark.parametrize("num_seqs,q_stride,seed", [(1, 6, 0), (64, 6, 1), (300, 8, 2), (5, 1, 3)])
+@pytest.mark.parametrize("num_seqs,q_stride,seed",
+                         [(1, 6, 0), (64, 6, 1), (300, 8, 2), (5, 1, 3), (0, 6, 4)])
 def test_commit_metadata_matches_oracle(K, cuda, num_seqs, q_stride, seed):
     """Device metadata of the draft's replay of the committed tails:
     bit-exact against the restatement, from accept lengths taken straight
@@ -525,7 +527,7 @@ def test_commit_metadata_matches_oracle(K, cuda, num_seqs, q_stride, seed):
     start = g.integers(0, bs * (width - 1) - 16, num_seqs).astype(np.int32)
     tables = g.integers(0, 5000, (num_seqs, width)).astype(np.int32)
     tables[g.random((num_seqs, width)) < 0.05] = -1
-    t = num_seqs * q_stride
+    t = max(num_seqs * q_stride, 5)
     argmax = g.integers(0, 151936, t).astype(np.int32)
     ref = oracle.commit_metadata(start, accept, q_stride, argmax, tables, bs, t)
     d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
