@@ -1019,6 +1019,18 @@ def main():
 
     from nanovllm_amd import kernels
 
+    # Each hot-path kernel alone, first while the process is fresh: after an
+    # engine has been built, run and released in the same process, the
+    # streaming kernels read slower on memory allocated afterwards (K4 at
+    # config 3's verify rows 20.9-21.2 -> 23.1-23.9 us, K1 at config 3
+    # 61.1-61.3 -> 63.1-67.1 us, same code and shapes).  The engine's own
+    # buffers are allocated in a fresh process, so the fresh figures are the
+    # kernels'; the same records after the engines are kept beside them.
+    per_config = None
+    if not args.no_per_config:
+        per_config = kernel_configs(args, 0.0 if args.no_cpu_baseline else 4.0)
+        torch.cuda.empty_cache()
+
     timer = AttnTimer()
     timer.wrap(kernels)
 
@@ -1113,9 +1125,10 @@ def main():
         forced = forced_acceptance(args, tmp, continuations)
         log(f"forced acceptance: {forced['value']} tok/s, {forced['ms_per_step']} ms/step, "
             f"mean acceptance length {forced['mean_acceptance_length']}")
-    per_config = None
+    per_config_after = None
     if not args.no_per_config:
-        per_config = kernel_configs(args, 0.0 if args.no_cpu_baseline else 4.0)
+        per_config_after = [{k: v for k, v in rec.items() if k != "cpu_baseline"}
+                            for rec in kernel_configs(args, 0.0)]
 
     result = {
         "metric": METRIC,
@@ -1147,6 +1160,11 @@ def main():
         "reference_pipeline": ref,
         "reference_pipeline_torch_attention": ref_torch,
         "per_config": per_config,
+        "per_config_after_engines": per_config_after,
+        "per_config_note": "per_config: each kernel alone at the BASELINE configs' shapes, timed "
+                           "before any engine ran in this process; per_config_after_engines: the "
+                           "same records after the engines were built, run and released (memory "
+                           "allocated after that reads slower)" if per_config else None,
         "setup_s": round(setup_s, 1),
     }
     print(json.dumps(result), flush=True)
