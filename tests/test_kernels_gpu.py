@@ -361,6 +361,28 @@ def test_verify_attention_bf16(K, cuda, name, kw):
     assert err <= ATTN_TOL, (name, err)
 
 
+@pytest.mark.parametrize("block_size", [32, 64, 128])
+@pytest.mark.parametrize("name,kw,fp8", [
+    # eight waves per split; with small pages a split holds at most 62 pages,
+    # so long sequences take several splits and the combine
+    ("q6_gqa4", dict(seed=30, batch=8, q_len=6, ctx_lo=30, ctx_hi=3000, hq=32, hkv=8), False),
+    # FP8 stream ranges across page boundaries
+    ("q5_gqa2_fp8", dict(seed=31, batch=10, q_len=5, ctx_lo=40, ctx_hi=2600, hq=16, hkv=8), True),
+    # 64-row tiles, one wave per split
+    ("q8_gqa8", dict(seed=32, batch=4, q_len=8, ctx_lo=100, ctx_hi=2500, hq=64, hkv=8), False),
+    ("decode", dict(seed=33, batch=10, q_len=1, ctx_lo=1, ctx_hi=2000, hq=32, hkv=8), False),
+])
+def test_verify_attention_small_pages(K, cuda, block_size, name, kw, fp8):
+    """Pages of 32, 64 and 128 tokens (the ABI takes any multiple of 32): the
+    same store + attention against the oracle, so the per-split page limit,
+    the chunk-to-page addressing and the combine hold off the 256-token
+    default too."""
+    case = paged_case(block_size=block_size, **kw)
+    got, ref = _run_verify(K, cuda, case, fp8=fp8)
+    err = np.abs(got - ref).max()
+    assert err <= ATTN_TOL, (name, block_size, err)
+
+
 def test_verify_attention_fp8(K, cuda):
     case = paged_case(seed=7, batch=8, q_len=5, ctx_lo=300, ctx_hi=3000, hq=16, hkv=8)
     got, ref = _run_verify(K, cuda, case, fp8=True)
