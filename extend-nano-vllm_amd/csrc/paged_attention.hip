@@ -13,7 +13,7 @@
 //     the same number of keys whatever the length mix;
 //   * fixed (everything else): one workgroup per (kv head, sequence, query
 //     tile, key split).  For bf16 tiles of up to 32 rows eight waves share a
-//     2560-key split (wave w takes chunks w, w+8, ...) and fold their
+//     2688-key split (wave w takes chunks w, w+8, ...) and fold their
 //     softmax states together in LDS; otherwise one wave runs a 3072-key
 //     split (both lengths follow the batch, see choose_split).
 // A sequence covered by one segment gets bf16 output directly; otherwise
@@ -59,7 +59,7 @@ constexpr int kChunk = 32;
 constexpr int kVPitch = 68;                          // dwords per staged V row
 constexpr int kVStage = kChunk * kVPitch;            // dwords of the wave's V stage
 constexpr int kSplitKeys = 3072;       // fixed decomposition, one wave per split
-constexpr int kKeysPerSharedWave = 320; // fixed decomposition, several waves per split
+constexpr int kKeysPerSharedWave = 336; // fixed decomposition, several waves per split
 constexpr int kMinSplit = 128;
 constexpr int64_t kMinWaves = 1024;
 // a split spans at most kWave - 2 blocks; blocks hold at least kChunk tokens
@@ -887,8 +887,8 @@ int32_t device_cus() {
 
 // Split length of the fixed decomposition.  A segment is one (sequence, kv
 // head, query tile); `waves` waves share each split.
-//   * Eight waves per split (bf16 tiles of up to 32 rows): 320 keys per
-//     wave, 2560 per split; when the batch has at least four segments per
+//   * Eight waves per split (bf16 tiles of up to 32 rows): 336 keys per
+//     wave, 2688 per split; when the batch has at least four segments per
 //     CU (several rounds of workgroups, which the dispatcher balances), one
 //     split covers the whole sequence instead (no fp32 partials, no
 //     combine, each workgroup streams longer).
@@ -901,9 +901,11 @@ int32_t device_cus() {
 // run): Qwen3-32B verify (64-row tiles, keys 2-8k) 521 us at 3072, 545 at
 // 4096, 484-487 at 6144, 590 at 8192 (one round of unequal waves); Qwen3-32B
 // draft decode (8-row tiles, 1024 segments) 431 us at 3072, 414 whole;
-// Qwen3-0.6B verify (256 segments, one round, keys up to 4k) 58.9-59.5 us
-// at 2560, 60.2-60.3 at 3072, 64.4 at 2048, 64.3 whole (the longest
-// segments alone set the time).  The length shrinks in 128-key steps (to a 128-key
+// Qwen3-0.6B verify (256 segments, one round, keys 512-4096) 58.0-58.3 us
+// at 2688, 58.4-58.5 at 2816, 59.6 at 2560, 60.1-60.9 at 3072, 61.5-62.4 at
+// 2304, 64.4 at 2048, 64.3 whole: in one round the split balances the
+// longest first splits against a short sequence plus the longest second
+// split, each workgroup's start-up worth ~340 keys of streaming.  The length shrinks in 128-key steps (to a 128-key
 // minimum) only while fewer than kMinWaves waves would be launched, and is
 // capped so that a split spans at most kWave - 2 blocks of block_size tokens
 // (the kernel holds one block id per lane); block_size 0 (unknown: the
