@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import acceptance_logits, bits, from_bits, paged_case
+from helpers import acceptance_logits, bits, paged_case
 from oracle import oracle
 
 pytestmark = pytest.mark.gpu

@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 import torch
 
-from helpers import acceptance_logits, bits, from_bits, paged_case
+from helpers import acceptance_logits, bits, paged_case
 from oracle import oracle
 
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
