@@ -14,10 +14,10 @@ The same JSON line carries
                  (the timed steps replay HIP graphs, inside which ROCm torch
                  cannot record timing events), and its 36 verify-attention
                  launches, --roofline-repeats times over, are captured in a
-                 HIP graph whose replay is timed between two events (so the
-                 host's launch rate cannot pace them); achieved = algorithmic
-                 bytes per launch /
-                 mean launch time, algorithmic bytes = sum_i L_i*Hkv*D*2B*2
+                 HIP graph whose replays are timed between events (so the
+                 host's launch rate cannot pace them; the median of three
+                 replays); achieved = algorithmic bytes per launch / mean
+                 launch time, algorithmic bytes = sum_i L_i*Hkv*D*2B*2
                  (K and V read once) + T*Hq*D*2B*2 (Q in, O out);
   cpu_baseline:  the reference's host acceptance logic (per-sequence bf16
                  argmax + .tolist() + verify_greedy_proposals) timed on this
@@ -28,6 +28,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import sys
 import tempfile
@@ -120,10 +121,11 @@ class AttnTimer:
     forward (launched eagerly) is recorded with its arguments and its
     algorithmic bytes, computed from the host-side metadata.  ``measure``
     then captures those exact launches, ``repeats`` times over, in a HIP
-    graph and times one replay on the current stream (the one the kernels
-    are enqueued on) between two HIP events, so that the mean launch time is
-    the kernels' own time and not the host's launch rate.  The re-issued
-    launches only read the K/V cache and write fresh output buffers."""
+    graph and times three replays on the current stream (the one the kernels
+    are enqueued on) between HIP events, so that the mean launch time (of the
+    median replay) is the kernels' own time and not the host's launch rate.
+    The re-issued launches only read the K/V cache and write fresh output
+    buffers."""
 
     def __init__(self):
         self.capture = False
@@ -175,15 +177,20 @@ class AttnTimer:
         graph.replay()
         torch.cuda.synchronize()
         stream = torch.cuda.current_stream()
-        s = torch.cuda.Event(enable_timing=True)
-        e = torch.cuda.Event(enable_timing=True)
-        s.record(stream)
-        graph.replay()
-        e.record(stream)
-        torch.cuda.synchronize()
+        # the median of three replays: the same launches run a few percent
+        # slower through some stretches of a few ms
+        replay_ms = []
+        for _ in range(3):
+            s = torch.cuda.Event(enable_timing=True)
+            e = torch.cuda.Event(enable_timing=True)
+            s.record(stream)
+            graph.replay()
+            e.record(stream)
+            torch.cuda.synchronize()
+            replay_ms.append(s.elapsed_time(e))
         del graph
         launches = repeats * len(self.calls)
-        mean_ms = s.elapsed_time(e) / launches
+        mean_ms = sorted(replay_ms)[1] / launches
         mean_bytes = sum(self.bytes) / len(self.bytes)
         gbs = mean_bytes / (mean_ms * 1e-3) / 1e9
         self.calls = []
@@ -191,7 +198,7 @@ class AttnTimer:
                 "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": traffic,
                 "kernel": "paged_attention_kernel (+ combine_kernel when a sequence is split): one "
                           "verify-attention call",
-                "launches": launches, "mean_us": round(mean_ms * 1e3, 2),
+                "launches": launches, "replays": 3, "mean_us": round(mean_ms * 1e3, 2),
                 "bytes_per_launch": int(mean_bytes)}
 
 
@@ -449,10 +456,11 @@ def kernel_configs(args, cpu_seconds: float = 0.0) -> list:
     one record per (kernel, config).
 
     Seeds follow the configs' order (config 1: 0 ... config 5: 4).  Inputs
-    are device-resident before timing.  ``iters`` launches are captured in a
-    HIP graph, so that the host's launch latency does not pace the small
-    kernels, and each figure is one replay between two HIP events on the
-    replay stream, divided by ``iters``.
+    are device-resident before timing.  Each kernel's launches are captured
+    in a HIP graph, so that the host's launch latency does not pace the small
+    kernels, as many as make one replay last >= 20 ms (30 to 2000 launches),
+    and each figure is the median of three replays between HIP events on the
+    replay stream, divided by the launches per replay.
     Algorithmic bytes per launch:
       K1 attention: sum_i L_i*Hkv*D*esz*2 + T*Hq*D*2*2 (config 5: logical
                     bytes; its prefix-shared pages are read once per sharer);
@@ -473,17 +481,18 @@ def kernel_configs(args, cpu_seconds: float = 0.0) -> list:
     V = QWEN3_PRESETS["qwen3-8b"]["vocab_size"]
     D, BS = 128, 256
 
-    def timed(fn, iters=30):
-        for _ in range(3):
-            fn()
-        torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+
+    def capture(fn, iters):
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
             for _ in range(iters):
                 fn()
         graph.replay()
         torch.cuda.synchronize()
-        stream = torch.cuda.current_stream()
+        return graph
+
+    def replay_us(graph, iters):
         s = torch.cuda.Event(enable_timing=True)
         e = torch.cuda.Event(enable_timing=True)
         s.record(stream)
@@ -492,17 +501,40 @@ def kernel_configs(args, cpu_seconds: float = 0.0) -> list:
         torch.cuda.synchronize()
         return s.elapsed_time(e) / iters * 1e3
 
+    def timed(fn, min_ms=20.0, max_iters=2000, replays=3):
+        """(mean launch time in us, launches per replay).  The burst is sized
+        from a 30-launch replay so that one replay runs >= min_ms: on MI355X
+        the same launches run a few percent slower through some stretches of
+        a few ms (a 300-launch trace of config 3's attention: 58-59 us, then
+        70 launches at 62.2, then 59.5; the next replay 58.05 throughout), so
+        a 2 ms window reads 60-63 us where 20 ms windows read 57.7-57.9.
+        The median of ``replays`` replays is returned."""
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        iters = 30
+        graph = capture(fn, iters)
+        want = min(max_iters, max(iters, math.ceil(min_ms * 1e3 / replay_us(graph, iters))))
+        if want > iters:
+            del graph
+            iters = want
+            graph = capture(fn, iters)
+        us = statistics.median(replay_us(graph, iters) for _ in range(replays))
+        del graph
+        return us, iters
+
     records = []
 
     def wanted(config):
         return args.kernel_filter in config
 
-    def emit(kernel, config, us, byts, **extra):
+    def emit(kernel, config, timing, byts, **extra):
+        us, launches = timing
         gbs = byts / us / 1e3
         records.append({"kernel": kernel, "config": config, "us": round(us, 2),
                         "bytes": int(byts), "GBs": round(gbs, 1),
-                        "frac": round(gbs / HBM_PEAK_GBS, 4), **extra})
-        log(f"kernel {kernel} / {config}: {us:.2f} us")
+                        "frac": round(gbs / HBM_PEAK_GBS, 4), "launches": launches, **extra})
+        log(f"kernel {kernel} / {config}: {us:.2f} us ({launches} launches per replay)")
 
     def cpu_acceptance(lg_cpu, q_len, batch, ids_cpu):
         """The reference's per-sequence argmax + verify on the host, timed
@@ -589,12 +621,12 @@ def kernel_configs(args, cpu_seconds: float = 0.0) -> list:
                                            c["cu_k"], c["q_len"], max(c["lens"]), D ** -0.5,
                                            c["bt"], k_scale=one, v_scale=one, out=out)
 
-        us = timed(call)
+        timing = timed(call)
         byts = sum(c["lens"]) * c["hkv"] * D * esz * 2 + c["T"] * c["hq"] * D * 2 * 2
         extra = {}
         if c["phys"] < sum(c["lens"]) * c["hkv"] * D * esz * 2:
             extra["unique_kv_bytes"] = int(c["phys"])
-        emit("K1 paged_attention_varlen", name, us, byts, batch=len(c["lens"]), q_len=c["q_len"],
+        emit("K1 paged_attention_varlen", name, timing, byts, batch=len(c["lens"]), q_len=c["q_len"],
              heads=f"{c['hq']}/{c['hkv']}", kv="fp8" if c["fp8"] else "bf16",
              sum_seqlen_k=sum(c["lens"]), kv_layout=args.kv_layout,
              batch_order=args.batch_order, **extra)
@@ -606,9 +638,9 @@ def kernel_configs(args, cpu_seconds: float = 0.0) -> list:
         qkv = torch.randn(T, (c["hq"] + 2 * hkv) * D, device=dev).to(torch.bfloat16)
         key = qkv[:, c["hq"] * D:(c["hq"] + hkv) * D].view(T, hkv, D)
         value = qkv[:, (c["hq"] + hkv) * D:].view(T, hkv, D)
-        us = timed(lambda: kernels.store_kvcache(key, value, c["kc"], c["vc"], c["slots"], one,
+        timing = timed(lambda: kernels.store_kvcache(key, value, c["kc"], c["vc"], c["slots"], one,
                                                  one))
-        emit("K2 store_kvcache", name, us, T * hkv * D * (2 + esz) * 2, rows=T)
+        emit("K2 store_kvcache", name, timing, T * hkv * D * (2 + esz) * 2, rows=T)
 
     def rollback(name, c):
         g = torch.Generator().manual_seed(7)
@@ -616,8 +648,8 @@ def kernel_configs(args, cpu_seconds: float = 0.0) -> list:
         acc = torch.randint(0, c["q_len"], (b,), generator=g).to(torch.int32).to(dev)
         slots = c["slots"].clone()
         seqlens = torch.tensor(c["lens"], dtype=torch.int32, device=dev)
-        us = timed(lambda: kernels.rollback(c["cu_q"], acc, slots, seqlens))
-        emit("K2 rollback (slots only)", name, us, b * 4 * 3 + c["T"] * 4, seqs=b,
+        timing = timed(lambda: kernels.rollback(c["cu_q"], acc, slots, seqlens))
+        emit("K2 rollback (slots only)", name, timing, b * 4 * 3 + c["T"] * 4, seqs=b,
              on_step=False)
 
     # config 1: greedy acceptance, [8, 5, V] logits, drafts raised with p = 0.7
@@ -636,11 +668,11 @@ def kernel_configs(args, cpu_seconds: float = 0.0) -> list:
         ids_cpu = torch.cat([torch.randint(0, V, (batch, 1), generator=g), prop], 1).reshape(-1)
         ids = ids_cpu.to(dev)
         cu = torch.arange(0, batch * q_len + 1, q_len, dtype=torch.int32, device=dev)
-        us = timed(lambda: kernels.argmax_accept(lg, cu, ids))
+        timing = timed(lambda: kernels.argmax_accept(lg, cu, ids))
         extra = {}
         if cpu_seconds > 0:
             extra["cpu_baseline"] = cpu_acceptance(lg_cpu, q_len, batch, ids_cpu)
-        emit("K4 argmax_accept", name, us, batch * q_len * V * 2, rows=batch * q_len, vocab=V,
+        emit("K4 argmax_accept", name, timing, batch * q_len * V * 2, rows=batch * q_len, vocab=V,
              **extra)
 
     if wanted("config1 B8 k4"):
@@ -663,8 +695,8 @@ def kernel_configs(args, cpu_seconds: float = 0.0) -> list:
         hid = [torch.randn(c3["T"], H, device=dev).to(torch.bfloat16) for _ in range(3)]
         res = [torch.randn(c3["T"], H, device=dev).to(torch.bfloat16) for _ in range(3)]
         src = torch.arange(c3["T"], dtype=torch.int32, device=dev)
-        us = timed(lambda: kernels.aux_gather(hid, res, src))
-        emit("K3 aux_gather", "config3 B64 q6 R=384 H=4096 3 layers", us, c3["T"] * 3 * H * 2 * 3)
+        timing = timed(lambda: kernels.aux_gather(hid, res, src))
+        emit("K3 aux_gather", "config3 B64 q6 R=384 H=4096 3 layers", timing, c3["T"] * 3 * H * 2 * 3)
         del c3, hid, res
     if wanted("config3 draft decode B64 q1"):
         dec = pages(5, 64, 1, 256, 2304, 32, 8, copies=4)
