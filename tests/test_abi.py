@@ -37,6 +37,48 @@ def test_binding_covers_the_header():
     assert sorted(_native.SIGNATURES) == declared_symbols()
 
 
+_C_TYPES = {"int32_t": ctypes.c_int32, "int64_t": ctypes.c_int64, "int": ctypes.c_int,
+            "float": ctypes.c_float, "size_t": ctypes.c_size_t}
+
+
+def header_signatures():
+    """(restype, argtypes) of every declaration in the header, from its C
+    parameter types: pointers are c_void_p (c_char_p for a returned string)."""
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    sigs = {}
+    for ret, name, params in re.findall(r"([\w ]+?\s*\*?)\s*\b(nva_\w+)\s*\(([^)]*)\)\s*;", text):
+        ret = ret.strip()
+        restype = ctypes.c_char_p if "char" in ret and "*" in ret else _C_TYPES[ret.split()[-1]]
+        args = []
+        for prm in params.split(","):
+            prm = prm.strip()
+            if prm in ("", "void"):
+                continue
+            args.append(ctypes.c_void_p if "*" in prm else _C_TYPES[prm.split()[-2]])
+        sigs[name] = (restype, args)
+    return sigs
+
+
+def test_binding_matches_the_header_types():
+    sigs = header_signatures()
+    assert sorted(sigs) == declared_symbols()
+    for name, (restype, argtypes) in _native.SIGNATURES.items():
+        assert sigs[name] == (restype, argtypes), name
+
+
+def test_integration_doc_argtypes_match_the_header():
+    """Every `_lib.nva_*.argtypes = [...]` line of INTEGRATION.md's ctypes
+    snippets declares the header's parameter types."""
+    doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    names = {"P": ctypes.c_void_p, "I32": ctypes.c_int32, "I64": ctypes.c_int64,
+             "INT": ctypes.c_int, "F32": ctypes.c_float, "SZ": ctypes.c_size_t}
+    found = re.findall(r"_lib\.(nva_\w+)\.argtypes\s*=\s*(\[[^\]]*\](?:\s*\*\s*\d+)?)", doc)
+    assert len(found) >= 10
+    for name, expr in found:
+        argtypes = eval(expr, {"__builtins__": {}}, names)
+        assert argtypes == _native.SIGNATURES[name][1], name
+
+
 def test_host_side_argument_errors_without_gpu():
     lib = _native.load()
     assert lib.nva_version().startswith(b"nanovllm_amd")
