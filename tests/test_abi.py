@@ -67,8 +67,8 @@ def test_binding_matches_the_header_types():
 
 
 def test_integration_doc_argtypes_match_the_header():
-    """Every `_lib.nva_*.argtypes = [...]` line of INTEGRATION.md's ctypes
-    snippets declares the header's parameter types."""
+    """Every `_lib.nva_*.argtypes = [...]` line of the integration guide's
+    ctypes snippets declares the header's parameter types."""
     doc = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     names = {"P": ctypes.c_void_p, "I32": ctypes.c_int32, "I64": ctypes.c_int64,
              "INT": ctypes.c_int, "F32": ctypes.c_float, "SZ": ctypes.c_size_t}
