@@ -335,12 +335,21 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
     // alone and LDS executes a wave's operations in order, so a compiler
     // barrier plus an LDS wait (before the first read) orders them.
     if (FP8) {
+      // Lane l stages 16 values of row 8 i + l / 8 as two 16-byte halves
+      // at dwords 8 (l % 8) and + 4.  A 16-byte LDS store serves eight
+      // lanes per cycle over 32 four-byte banks, so if every lane stored
+      // its first half first, lanes l and l + 4 would share a bank group
+      // (2-way conflicts on every store).  Lanes 4-7 of each eight store
+      // their second half first: each store's eight lanes then cover all
+      // 32 banks.
+      const bool swap = (lane >> 2) & 1;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int row = 8 * i + (lane >> 3);
         uint32_t* dst = stage + row * kVPitch + (lane & 7) * 8;
-        *reinterpret_cast<bf16x8_t*>(dst) = fp8x8_to_bf16(make_uint2(ch.v[i].x, ch.v[i].y));
-        *reinterpret_cast<bf16x8_t*>(dst + 4) = fp8x8_to_bf16(make_uint2(ch.v[i].z, ch.v[i].w));
+        const uint2 lo = make_uint2(ch.v[i].x, ch.v[i].y), hi = make_uint2(ch.v[i].z, ch.v[i].w);
+        *reinterpret_cast<bf16x8_t*>(dst + (swap ? 4 : 0)) = fp8x8_to_bf16(swap ? hi : lo);
+        *reinterpret_cast<bf16x8_t*>(dst + (swap ? 0 : 4)) = fp8x8_to_bf16(swap ? lo : hi);
       }
     } else {
 #pragma unroll
