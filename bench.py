@@ -469,7 +469,10 @@ def kernel_configs(args, cpu_seconds: float = 0.0) -> list:
       K4 argmax:    rows*V*2 read.
     With cpu_seconds > 0, the acceptance configs also time the reference's
     host acceptance logic (oracle.reference_cpu_acceptance) on the same
-    seeded bf16 bytes the kernel reads, with every host core and with one."""
+    seeded bf16 bytes the kernel reads, with every host core and with one,
+    and the attention records of configs 2 and 4 time the CPU oracle's
+    textbook attention on their own pages (config 2 whole, config 4 every
+    32nd sequence; one thread) as context."""
     import statistics
 
     import torch
@@ -608,7 +611,39 @@ def kernel_configs(args, cpu_seconds: float = 0.0) -> list:
         return dict(lens=lens, kc=kc, vc=vc, kv=kv, q=q, cu_q=cu_q, cu_k=cu_k, bt=bt.to(dev),
                     slots=slots, T=T, q_len=q_len, hq=hq, hkv=hkv, fp8=fp8, phys=phys)
 
-    def attention(name, c):
+    def cpu_attention(c, every):
+        """The CPU oracle's textbook paged attention (double accumulation,
+        one thread) on every `every`-th sequence of the config's own pages
+        and queries, for context beside K1 (BASELINE configs 2 and 4; not a
+        target).  The copies to host memory are not timed."""
+        import numpy as np
+        from oracle import oracle
+
+        sel = list(range(0, len(c["lens"]), every))
+        q_len = c["q_len"]
+        if c["fp8"]:
+            def bits(x):
+                return x.contiguous().view(torch.uint8).numpy()
+        else:
+            def bits(x):
+                return x.contiguous().view(torch.int16).numpy().view(np.uint16)
+        kc, vc = bits(c["kv"][0, 0].cpu()), bits(c["kv"][0, 1].cpu())
+        rows = [i * q_len + j for i in sel for j in range(q_len)]
+        q = c["q"].cpu()[rows].contiguous().view(torch.int16).numpy().view(np.uint16)
+        lens = [c["lens"][i] for i in sel]
+        bt = c["bt"].cpu()[sel].numpy()
+        cu = np.arange(0, len(sel) * q_len + 1, q_len, dtype=np.int32)
+        t0 = time.perf_counter()
+        oracle.paged_attention(q, kc, vc, cu, lens, bt, D ** -0.5)
+        dt = time.perf_counter() - t0
+        keys, total = sum(lens), sum(c["lens"])
+        return {"kind": "port", "threads": 1, "seconds": round(dt, 3),
+                "sample": f"sequences 0, {every}, {2 * every}, ...: {len(sel)} of "
+                          f"{len(c['lens'])}, {keys} of {total} keys",
+                "us_per_call_scaled_to_batch": round(dt * 1e6 * total / keys, 1),
+                "keys_per_s": round(keys / dt, 1)}
+
+    def attention(name, c, cpu_every=0):
         esz = 1 if c["fp8"] else 2
         one = torch.ones(1, device=dev) if c["fp8"] else None
         out = torch.empty_like(c["q"])
@@ -626,6 +661,8 @@ def kernel_configs(args, cpu_seconds: float = 0.0) -> list:
         extra = {}
         if c["phys"] < sum(c["lens"]) * c["hkv"] * D * esz * 2:
             extra["unique_kv_bytes"] = int(c["phys"])
+        if cpu_every and cpu_seconds > 0:
+            extra["cpu_oracle"] = cpu_attention(c, cpu_every)
         emit("K1 paged_attention_varlen", name, timing, byts, batch=len(c["lens"]), q_len=c["q_len"],
              heads=f"{c['hq']}/{c['hkv']}", kv="fp8" if c["fp8"] else "bf16",
              sum_seqlen_k=sum(c["lens"]), kv_layout=args.kv_layout,
@@ -683,7 +720,7 @@ def kernel_configs(args, cpu_seconds: float = 0.0) -> list:
     if wanted("config2 B32 q5"):
         c2 = pages(1, 32, 5, 512, 4096, 16, 8, copies=4)
         store("config2 B32 q5", c2)
-        attention("config2 B32 q5 Qwen3-0.6B", c2)
+        attention("config2 B32 q5 Qwen3-0.6B", c2, cpu_every=1)
         rollback("config2 B32 q5", c2)
         del c2
 
@@ -706,7 +743,7 @@ def kernel_configs(args, cpu_seconds: float = 0.0) -> list:
     if wanted("config4 B128 q5 fp8"):
         c4 = pages(3, 128, 5, 4096, 16384, 16, 8, fp8=True)
         store("config4 B128 q5 fp8", c4)
-        attention("config4 B128 q5 fp8", c4)
+        attention("config4 B128 q5 fp8", c4, cpu_every=32)
         del c4
 
     if wanted("config5 B128 q8"):
