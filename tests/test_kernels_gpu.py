@@ -43,6 +43,21 @@ def test_argmax_accept_matches_oracle(K, cuda, batch, k, vocab, seed):
     np.testing.assert_array_equal(ref_am, logits.argmax(-1).numpy())
 
 
+def test_argmax_accept_on_the_committed_config1_fixture(K, cuda):
+    """K4 on BASELINE config 1's committed reduced-vocabulary fixture
+    (tests/golden/config1_reduced.npz), against its frozen outputs."""
+    import os
+    f = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                             "config1_reduced.npz"))
+    logits = torch.from_numpy(f["logits_bits"].view(np.int16)).view(torch.bfloat16).to(cuda)
+    am, acc, bonus = K.argmax_accept(logits, torch.from_numpy(f["cu_q"]).to(cuda),
+                                     torch.from_numpy(f["input_ids"]).to(cuda))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(am.cpu().numpy(), f["argmax"])
+    np.testing.assert_array_equal(acc.cpu().numpy(), f["accept_len"])
+    np.testing.assert_array_equal(bonus.cpu().numpy(), f["bonus"])
+
+
 @pytest.mark.parametrize("layout", ["odd_width", "aligned", "padded_rows"])
 def test_argmax_edge_values(K, cuda, layout):
     """NaN / signed zero / inf / denormal / tie cases on both partial kernels:

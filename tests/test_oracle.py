@@ -83,6 +83,19 @@ def test_accept_batch_matches_python_restatement():
     assert committed == int(acc.sum()) + 8
 
 
+def test_oracle_on_the_committed_config1_fixture():
+    """BASELINE config 1 at a reduced vocabulary, frozen with its expected
+    outputs (tests/golden/gen_config1_fixture.py: numpy argmax and a plain
+    first-mismatch scan, no oracle code)."""
+    f = np.load(os.path.join(GOLDEN, "config1_reduced.npz"))
+    am = oracle.argmax_bf16(f["logits_bits"])
+    np.testing.assert_array_equal(am, f["argmax"])
+    acc, bonus = oracle.accept(f["cu_q"], am, f["input_ids"])
+    np.testing.assert_array_equal(acc, f["accept_len"])
+    np.testing.assert_array_equal(bonus, f["bonus"])
+    assert set(f["accept_len"].tolist()) >= {0, 1, 4}   # none, partial and full acceptance
+
+
 def test_accept_empty_sequence():
     acc, bonus = oracle.accept(np.array([0, 0, 2], np.int32), np.array([4, 5], np.int32),
                                np.array([1, 4], np.int64))
