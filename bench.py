@@ -57,6 +57,25 @@ PMC_WORKLOAD = dict(preset="qwen3-8b", batch=64, k=5, prompt_min=256, prompt_max
 METRIC = "accepted tok/s, Qwen3-8B EAGLE3 k=5 bs64; verify-attn HBM GB/s % of peak"
 
 
+def workload_label(args) -> tuple:
+    """(metric, workload) of the bench line for the chosen preset, batch and
+    k; the default workload keeps METRIC."""
+    from nanovllm_amd.synthetic import QWEN3_PRESETS, default_aux_layers
+
+    p = QWEN3_PRESETS[args.preset]
+    name = {"qwen3-8b": "Qwen3-8B", "qwen3-0.6b": "Qwen3-0.6B",
+            "qwen3-32b": "Qwen3-32B"}.get(args.preset, args.preset)
+    aux = "/".join(str(a) for a in default_aux_layers(args.preset))
+    workload = (f"EAGLE3 speculative decode step, {name} geometry ({p['num_hidden_layers']} "
+                f"layers, H{p['hidden_size']}, {p['num_attention_heads']}q/"
+                f"{p['num_key_value_heads']}kv, D{p['head_dim']}, MLP{p['intermediate_size']}, "
+                f"V{p['vocab_size']}), draft 1 layer + fc 3H->H on aux layers {aux}")
+    if (args.preset, args.k, args.batch) == ("qwen3-8b", 5, 64):
+        return METRIC, workload
+    return (f"accepted tok/s, {name} EAGLE3 k={args.k} bs{args.batch}; verify-attn HBM GB/s % "
+            f"of peak", workload)
+
+
 def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1199,8 +1218,9 @@ def main():
         per_config_after = [{k: v for k, v in rec.items() if k != "cpu_baseline"}
                             for rec in kernel_configs(args, 0.0)]
 
+    metric, workload = workload_label(args)
     result = {
-        "metric": METRIC,
+        "metric": metric,
         "value": round(committed / elapsed, 1),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -1212,9 +1232,7 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic (random-init weights, random prompt ids)",
-        "config": {"workload": "EAGLE3 speculative decode step, Qwen3-8B geometry (36 layers, "
-                               "H4096, 32q/8kv, D128, MLP12288, V151936), draft 1 layer + fc 3H->H "
-                               "on aux layers 2/18/33",
+        "config": {"workload": workload,
                    "preset": args.preset, "batch": args.batch, "k": args.k,
                    "prompt_len": [args.prompt_min, args.prompt_max],
                    "max_tokens": args.max_tokens, "active_seqs": n_active,
