@@ -20,6 +20,7 @@ token.)
 """
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from nanovllm_amd import _native
@@ -27,7 +28,7 @@ from nanovllm_amd import kernels as K
 from nanovllm_amd.context import get_context, reset_context, set_context
 from nanovllm_amd.eagle3 import Eagle3KVCache, load_eagle3_model
 from nanovllm_amd.engine.graphs import (CommitGraph, DeviceCommitGraph, ProposeGraph, VerifyGraph,
-                                        bucket_for)
+                                        block_table_array, bucket_for)
 from nanovllm_amd.engine.sequence import Sequence
 from nanovllm_amd.layers import Attention, init_random_, param_bytes
 from nanovllm_amd.loader import load_model
@@ -49,6 +50,10 @@ def _use_gemm_tuning(path: str) -> None:
 
 
 def _pinned(values, dtype) -> torch.Tensor:
+    if isinstance(values, np.ndarray):
+        out = torch.empty(values.shape, dtype=dtype, pin_memory=True)
+        out.copy_(torch.from_numpy(values))
+        return out
     return torch.tensor(values, dtype=dtype, pin_memory=True)
 
 
@@ -418,12 +423,22 @@ class ModelRunner:
         sequence that needs fewer proposals (limits[i] < steps, near its
         max_tokens) gets slot -1 in the steps past its own last one: those
         steps' tokens are discarded, and their positions may lie beyond the
-        pages reserved for it (reserve_speculation stops at max_tokens)."""
-        pos = [[len(seq) - 1 + s for seq in seqs] for s in range(steps - 1)]
-        slots = [[self._slot(seq, p) if s < lim - 1 else -1
-                  for seq, p, lim in zip(seqs, row, limits)] for s, row in enumerate(pos)]
-        ctx_lens = [[p + 1 for p in row] for row in pos]
-        return pos, slots, ctx_lens
+        pages reserved for it (reserve_speculation stops at max_tokens).
+        Arrays [steps - 1, len(seqs)] (int64 positions, int32 slots and
+        lengths); a slot whose page is not in the block table raises
+        IndexError, as the block-table lookup does."""
+        b = len(seqs)
+        lens = np.fromiter((len(seq) for seq in seqs), dtype=np.int64, count=b)
+        s = np.arange(max(steps - 1, 0), dtype=np.int64)[:, None]
+        pos = lens[None, :] - 1 + s
+        need = s < np.asarray(limits, dtype=np.int64)[None, :] - 1
+        bt, nblk = block_table_array([seq.block_table for seq in seqs])
+        blk = pos // self.block_size
+        if np.any(need & (blk >= nblk[None, :])):
+            raise IndexError("a draft position has no page in its block table")
+        ids = bt[np.arange(b)[None, :], np.minimum(blk, bt.shape[1] - 1)].astype(np.int64)
+        slots = np.where(need, ids * self.block_size + pos % self.block_size, -1).astype(np.int32)
+        return pos, slots, (pos + 1).astype(np.int32)
 
     def _use_graphs(self) -> bool:
         return not self.enforce_eager
