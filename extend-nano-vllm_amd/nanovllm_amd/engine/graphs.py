@@ -211,9 +211,12 @@ class ProposeGraph(_GraphBase):
         self.hidden = torch.zeros(bs, h, dtype=r.dtype, device=self.device)
         self.feedback = torch.zeros(bs, h, dtype=r.dtype, device=self.device)
         self.tokens = torch.zeros(k, bs, dtype=torch.int64, device=self.device)
-        self.i64 = _Staging({"pos": steps * bs}, torch.int64, self.device)
+        # the draft-state rows of the batch (gathered inside the graph) and
+        # the draft steps' metadata, one host->device copy per dtype
+        self.i64 = _Staging({"state": bs, "pos": steps * bs}, torch.int64, self.device)
         self.i32 = _Staging({"slots": steps * bs, "ctx": steps * bs, "bt": bs * self.max_blocks},
                             torch.int32, self.device)
+        self.i64.fill("state", [0] * bs)
         self.i64.fill("pos", [0] * (steps * bs))
         self.i32.fill("slots", [-1] * (steps * bs))
         self.i32.fill("ctx", [1] * (steps * bs))
@@ -230,6 +233,9 @@ class ProposeGraph(_GraphBase):
         slots = self.i32.dev_view("slots").view(-1, bs)
         ctx = self.i32.dev_view("ctx").view(-1, bs)
         bt = self.i32.dev_view("bt").view(bs, self.max_blocks)
+        state = self.i64.dev_view("state")
+        torch.index_select(r.state_hidden, 0, state, out=self.hidden)
+        torch.index_select(r.state_feedback, 0, state, out=self.feedback)
         draft.sample_greedy(self.hidden, out=self.tokens[0])
         feedback = self.feedback
         try:
@@ -241,15 +247,14 @@ class ProposeGraph(_GraphBase):
         finally:
             reset_context()
 
-    def run(self, state_slots: torch.Tensor, pos, slots, ctx, bt_rows) -> torch.Tensor:
-        """state_slots: device int64 [b] rows of the runner's draft-state table.
+    def run(self, state_rows, pos, slots, ctx, bt_rows) -> torch.Tensor:
+        """state_rows: host list of the sequences' rows in the runner's
+        draft-state table (the padding rows read row 0 and are discarded).
         pos/slots/ctx: host [k-1][b] (arrays or nested lists).  Returns tokens
         [k, bs] (device)."""
-        r = self.runner
-        b = state_slots.numel()
+        b = len(state_rows)
         bs = self.bs
-        torch.index_select(r.state_hidden, 0, state_slots, out=self.hidden[:b])
-        torch.index_select(r.state_feedback, 0, state_slots, out=self.feedback[:b])
+        self.i64.fill("state", list(state_rows) + [0] * (bs - b))
 
         def padded(values, dtype, fill):
             a = np.asarray(values, dtype=dtype).reshape(-1, b)

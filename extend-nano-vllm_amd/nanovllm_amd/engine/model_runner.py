@@ -458,16 +458,16 @@ class ModelRunner:
             return [[] for _ in seqs]
         lens = [len(seq) for seq in seqs]
         pos, slots, ctx_lens = self._draft_step_metadata(seqs, limits, steps)
-        state_rows = _pinned(self._state_rows(seqs), torch.int64).to(self.device, non_blocking=True)
+        rows = self._state_rows(seqs)
         bs = bucket_for(len(seqs))
         if self._use_graphs() and steps == k and bs is not None:
             graph = self._propose_graphs.get(bs)
             if graph is None:
                 graph = self._propose_graphs[bs] = ProposeGraph(self, bs, k)
-            tokens = graph.run(state_rows, pos, slots, ctx_lens,
-                               [seq.block_table for seq in seqs])
+            tokens = graph.run(rows, pos, slots, ctx_lens, [seq.block_table for seq in seqs])
             table = tokens[:, :len(seqs)].cpu().tolist()
         else:
+            state_rows = _pinned(rows, torch.int64).to(self.device, non_blocking=True)
             table = self._propose_eager(seqs, state_rows, steps, pos, slots, ctx_lens, lens)
         return [[table[s][i] for s in range(limits[i])] for i in range(len(seqs))]
 
@@ -590,14 +590,14 @@ class ModelRunner:
             return None
         lens = [len(seq) for seq in seqs]
         pos, slots, ctx_lens = self._draft_step_metadata(seqs, [k] * b, k)
-        state_rows = _pinned(self._state_rows(seqs), torch.int64).to(self.device, non_blocking=True)
         pgraph = self._propose_graphs.get(bs)
         if pgraph is None:
             pgraph = self._propose_graphs[bs] = ProposeGraph(self, bs, k)
         vgraph = self._verify_graphs.get(bs)
         if vgraph is None:
             vgraph = self._verify_graphs[bs] = VerifyGraph(self, bs, k + 1)
-        tokens = pgraph.run(state_rows, pos, slots, ctx_lens, [seq.block_table for seq in seqs])
+        tokens = pgraph.run(self._state_rows(seqs), pos, slots, ctx_lens,
+                            [seq.block_table for seq in seqs])
         if self.draft_override is not None:
             self.draft_override(seqs, tokens)
         if self._proposal_host.numel() < k * bs:
