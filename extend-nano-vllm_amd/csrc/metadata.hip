@@ -180,3 +180,55 @@ extern "C" int nva_commit_metadata(const int32_t* start_pos, const int32_t* acce
       block_size, cu_seqlens_q, cu_seqlens_k, positions, slot_mapping, num_tokens, ca);
   return launch_status();
 }
+
+// Draft-step metadata for a draft queued right behind a verify: column i of
+// bs (i < num_seqs a sequence, the rest padding), row s of steps.  One
+// thread per (s, i); each reads its sequence's accepted count from the
+// verify's accept output, so the draft's lengths follow the verified step
+// without the host.
+__global__ void __launch_bounds__(kMetaThreads)
+draft_metadata_kernel(const int64_t* __restrict__ lens, const int64_t* __restrict__ verify_row,
+                      const int32_t* __restrict__ accept_len, int32_t num_seqs, int32_t bs,
+                      int32_t steps, const int32_t* __restrict__ block_tables,
+                      int64_t bt_stride, int32_t max_blocks, int32_t block_size,
+                      int64_t* __restrict__ positions, int32_t* __restrict__ slot_mapping,
+                      int32_t* __restrict__ context_lens) {
+  const int idx = blockIdx.x * kMetaThreads + threadIdx.x;
+  if (idx >= steps * bs) return;
+  const int s = idx / bs, i = idx % bs;
+  int64_t pos = 0;
+  int32_t slot = -1;
+  if (i < num_seqs) {
+    const int64_t len = lens[i] + accept_len[verify_row[i]] + 1;
+    pos = len - 1 + s;
+    const int64_t blk = pos / block_size;
+    const int32_t id = pos >= 0 && blk < max_blocks
+                           ? block_tables[static_cast<int64_t>(i) * bt_stride + blk] : -1;
+    if (id >= 0) slot = static_cast<int32_t>(static_cast<int64_t>(id) * block_size + pos % block_size);
+  }
+  positions[idx] = pos;
+  slot_mapping[idx] = slot;
+  context_lens[idx] = static_cast<int32_t>(pos + 1);
+}
+
+extern "C" int nva_draft_metadata(const int64_t* lens, const int64_t* verify_row,
+                                  const int32_t* accept_len, int32_t num_seqs, int32_t bs,
+                                  int32_t steps, const int32_t* block_tables,
+                                  int64_t block_table_stride, int32_t max_blocks_per_seq,
+                                  int32_t block_size, int64_t* positions, int32_t* slot_mapping,
+                                  int32_t* context_lens, void* stream) {
+  if (num_seqs < 0 || bs < num_seqs || steps < 0 || block_size <= 0 || max_blocks_per_seq < 0 ||
+      block_table_stride < max_blocks_per_seq)
+    return NVA_ERR_ARG;
+  if (steps == 0 || bs == 0) return NVA_OK;
+  if (!positions || !slot_mapping || !context_lens) return NVA_ERR_ARG;
+  if (num_seqs > 0 && (!lens || !verify_row || !accept_len ||
+                       (max_blocks_per_seq > 0 && !block_tables)))
+    return NVA_ERR_ARG;
+  const int n = steps * bs;
+  draft_metadata_kernel<<<(n + kMetaThreads - 1) / kMetaThreads, kMetaThreads, 0,
+                          static_cast<hipStream_t>(stream)>>>(
+      lens, verify_row, accept_len, num_seqs, bs, steps, block_tables, block_table_stride,
+      max_blocks_per_seq, block_size, positions, slot_mapping, context_lens);
+  return launch_status();
+}

@@ -22,6 +22,7 @@ eagerly; results are identical either way.
 """
 from __future__ import annotations
 
+import gc
 import itertools
 import sys
 
@@ -113,17 +114,28 @@ class _GraphBase:
         process registers torch's CUDA generator and allocates its graph-safe
         seed/offset tensors.  Allocated under inference mode they would be
         inference tensors, and every later capture outside inference mode
-        (the caller's own graphs) would fail on their in-place update."""
+        (the caller's own graphs) would fail on their in-place update.
+
+        Python's cyclic garbage collector is off during the capture: a
+        collection there can free objects of an engine that is gone (pinned
+        host buffers, graphs), and their release is not allowed while the
+        stream captures."""
         body()
         torch.cuda.synchronize(self.device)
         ctx = torch.cuda.graph(self.graph, pool=self.runner.graph_pool)
         with torch.inference_mode(False):
             ctx.__enter__()
+        collecting = gc.isenabled()
+        gc.disable()
         try:
             body()
         except BaseException:
+            if collecting:
+                gc.enable()
             ctx.__exit__(*sys.exc_info())
             raise
+        if collecting:
+            gc.enable()
         ctx.__exit__(None, None, None)
         if self.runner.graph_pool is None:
             self.runner.graph_pool = self.graph.pool()
@@ -226,14 +238,15 @@ class ProposeGraph(_GraphBase):
         self._capture(self._body)
 
     def _body(self):
+        bs = self.bs
+        self._draft_loop(self.i64.dev_view("state"), self.i64.dev_view("pos").view(-1, bs),
+                         self.i32.dev_view("slots").view(-1, bs),
+                         self.i32.dev_view("ctx").view(-1, bs),
+                         self.i32.dev_view("bt").view(bs, self.max_blocks))
+
+    def _draft_loop(self, state, pos, slots, ctx, bt):
         r = self.runner
         draft = r.eagle3_model
-        bs = self.bs
-        pos = self.i64.dev_view("pos").view(-1, bs)
-        slots = self.i32.dev_view("slots").view(-1, bs)
-        ctx = self.i32.dev_view("ctx").view(-1, bs)
-        bt = self.i32.dev_view("bt").view(bs, self.max_blocks)
-        state = self.i64.dev_view("state")
         torch.index_select(r.state_hidden, 0, state, out=self.hidden)
         torch.index_select(r.state_feedback, 0, state, out=self.feedback)
         draft.sample_greedy(self.hidden, out=self.tokens[0])
@@ -268,6 +281,67 @@ class ProposeGraph(_GraphBase):
         self.i32.fill("bt", block_table_array(bt_rows, bs, self.max_blocks)[0])
         self.i64.upload()
         self.i32.upload()
+        self.graph.replay()
+        return self.tokens
+
+
+class ChainedProposeGraph(ProposeGraph):
+    """The next step's draft, queued right behind a VerifyGraph and its
+    DeviceCommitGraph, before the host has read the results: each
+    sequence's length after the step, len + accepted + 1, comes from the
+    verify's accept results on the device, and with it the draft steps'
+    positions, slots (through block tables the host reserved one step
+    ahead) and context lengths.  The draft states it starts from are the
+    ones the device commit just wrote.  The host checks the lengths once it
+    has the results and drafts again if they differ (a sequence finished,
+    or left the batch); positions this draft wrote K/V for are written
+    again before anything reads them (model_runner.py:1159-1213)."""
+
+    def __init__(self, runner, bs: int, k: int, vgraph: "VerifyGraph"):
+        self.vgraph = vgraph
+        super().__init__(runner, bs, k)
+
+    def _body(self):
+        r = self.runner
+        bs, k, mb = self.bs, self.k, self.max_blocks
+        steps = max(k - 1, 1)
+        dev = self.device
+        if not hasattr(self, "lens"):
+            # static inputs (host copies of the batch, natural order) and outputs
+            self.meta = _Staging({"state": bs, "lens": bs, "vrow": bs}, torch.int64, dev)
+            self.meta32 = _Staging({"bt": bs * mb}, torch.int32, dev)
+            self.meta.fill("state", [0] * bs)
+            self.meta.fill("lens", [0] * bs)
+            self.meta.fill("vrow", [0] * bs)
+            self.meta32.fill("bt", [-1] * (bs * mb))
+            self.meta.upload()
+            self.meta32.upload()
+            self.lens = self.meta.dev_view("lens")
+            self.cpos = torch.zeros(steps, bs, dtype=torch.int64, device=dev)
+            self.cslots = torch.zeros(steps, bs, dtype=torch.int32, device=dev)
+            self.cctx = torch.zeros(steps, bs, dtype=torch.int32, device=dev)
+        bt = self.meta32.dev_view("bt").view(bs, mb)
+        v = self.vgraph
+        # one launch: each column's length after the verified step (its
+        # accepted count read from the verify's accept output), then every
+        # draft step's position, slot and context; padding columns have an
+        # empty block-table row, so their slots are -1
+        K.draft_metadata(self.lens, self.meta.dev_view("vrow"), v.out[v.T:v.T + bs], bs, bt,
+                         r.block_size, self.cpos, self.cslots, self.cctx)
+        self._draft_loop(self.meta.dev_view("state"), self.cpos, self.cslots, self.cctx, bt)
+
+    def launch(self, state_rows, lens, vrows, bt_rows) -> torch.Tensor:
+        """Host lists in the batch's natural order: draft-state rows, the
+        lengths before the verified step, each sequence's row in the verify
+        batch, block tables (reserved one step ahead).  Padding rows get
+        length 0 (no K/V written).  Returns tokens [k, bs] (device)."""
+        b, bs = len(state_rows), self.bs
+        self.meta.fill("state", list(state_rows) + [0] * (bs - b))
+        self.meta.fill("lens", list(lens) + [0] * (bs - b))
+        self.meta.fill("vrow", list(vrows) + [0] * (bs - b))
+        self.meta32.fill("bt", block_table_array(bt_rows, bs, self.max_blocks)[0])
+        self.meta.upload()
+        self.meta32.upload()
         self.graph.replay()
         return self.tokens
 

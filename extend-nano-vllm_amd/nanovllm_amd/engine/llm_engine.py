@@ -51,6 +51,10 @@ class LLMEngine:
         # comparison runs: execute speculative steps with the reference's
         # structure (see _reference_speculative_step)
         self.reference_pipeline = False
+        # queue each step's successor draft behind its verify (see
+        # _speculative_step); off, every step drafts after the host's
+        # bookkeeping, as before
+        self.prelaunch_draft = True
         atexit.register(self.exit)
 
     def exit(self):
@@ -99,8 +103,15 @@ class LLMEngine:
         for seq in seqs:
             self.scheduler.reserve_speculation(seq)
         # the runner may enqueue the verify right behind the draft, so that
-        # the host's bookkeeping below overlaps the target forward
-        proposals = self.model_runner.call("propose_verify_eagle3_batch", seqs)
+        # the host's bookkeeping below overlaps the target forward, and the
+        # next step's draft behind both (prelaunch) when the batch will stay
+        # as it is: nothing waiting, every sequence two steps from its budget
+        k = self.scheduler.num_speculative_tokens
+        prelaunch = (self.prelaunch_draft and not self.scheduler.waiting
+                     and all(seq.max_tokens - seq.num_completion_tokens > 2 * k + 1
+                             for seq in seqs)
+                     and self.scheduler.reserve_lookahead(seqs))
+        proposals = self.model_runner.call("propose_verify_eagle3_batch", seqs, prelaunch)
         pipelined = proposals is not None
         if not pipelined:
             proposals = self.model_runner.call("propose_eagle3_batch", seqs)

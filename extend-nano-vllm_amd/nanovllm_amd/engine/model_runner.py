@@ -27,8 +27,9 @@ from nanovllm_amd import _native
 from nanovllm_amd import kernels as K
 from nanovllm_amd.context import get_context, reset_context, set_context
 from nanovllm_amd.eagle3 import Eagle3KVCache, load_eagle3_model
-from nanovllm_amd.engine.graphs import (CommitGraph, DeviceCommitGraph, ProposeGraph, VerifyGraph,
-                                        block_table_array, bucket_for)
+from nanovllm_amd.engine.graphs import (ChainedProposeGraph, CommitGraph, DeviceCommitGraph,
+                                        ProposeGraph, VerifyGraph, block_table_array,
+                                        bucket_for)
 from nanovllm_amd.engine.sequence import Sequence
 from nanovllm_amd.layers import Attention, init_random_, param_bytes
 from nanovllm_amd.loader import load_model
@@ -98,6 +99,7 @@ class ModelRunner:
             self._propose_graphs: dict[int, ProposeGraph] = {}
             self._commit_graphs: dict[tuple[int, int], CommitGraph] = {}
             self._device_commit_graphs: dict[int, DeviceCommitGraph] = {}
+            self._chained_graphs: dict[int, ChainedProposeGraph] = {}
             self._device_committed = None
             self._pending_verify = None
             self._pending_graph = None
@@ -141,6 +143,11 @@ class ModelRunner:
         # tokens [k, bucket] in place before they are verified
         self.draft_override = None
         self._inflight_verify = None
+        # the next step's draft queued behind a verify (propose_verify_eagle3_batch
+        # with prelaunch): (graph, seq ids, lengths before the step, lengths
+        # after it once collect has the results)
+        self._prelaunched = None
+        self.prelaunch_stats = {"queued": 0, "used": 0}
         self._proposal_host = torch.empty(0, dtype=torch.int64)
         # one pinned host buffer receives argmax + accept results each verify
         self._verify_host = torch.empty(1 << 16, dtype=torch.int32, pin_memory=True)
@@ -191,6 +198,10 @@ class ModelRunner:
         self._device_commit_graphs.clear()
         self._verify_graphs.clear()
         self._propose_graphs.clear()
+        self._chained_graphs.clear()
+        self._prelaunched = None
+        self._inflight_verify = None
+        self._device_committed = None
 
     # ------------------------------------------------------------ memory
 
@@ -568,7 +579,7 @@ class ModelRunner:
         return out_t, out_a, out_b
 
     @torch.inference_mode()
-    def propose_verify_eagle3_batch(self, seqs: list[Sequence]):
+    def propose_verify_eagle3_batch(self, seqs: list[Sequence], prelaunch: bool = False):
         """Proposals and verification in one pass over the stream: the draft
         graph runs, its tokens are copied to the host, and the verify graph
         is enqueued behind them with its input ids composed on the device
@@ -579,25 +590,40 @@ class ModelRunner:
         do not cover the step (ragged proposal counts near max_tokens, no
         bucket, or graphs off), and the caller then proposes and verifies in
         turn.  The block tables must not change in between (the drafts'
-        blocks are reserved before proposing, as in the reference)."""
+        blocks are reserved before proposing, as in the reference).
+
+        prelaunch: also queue the next step's draft (ChainedProposeGraph)
+        behind this step's verify and device commit, so that it runs while
+        the host works through the results; the caller has reserved pages
+        for it (Scheduler.reserve_lookahead).  The next call uses those
+        proposals if its batch and lengths are the ones the results imply,
+        and drafts again otherwise."""
         assert self.eagle3_model is not None
         k = self.speculative_config.num_speculative_tokens
         b = len(seqs)
         bs = bucket_for(b)
+        pre, self._prelaunched = self._prelaunched, None
         if (not self.pipeline_verify or not self._use_graphs() or not self.use_verify_graph
                 or self.keep_verify_inputs or bs is None or k < 1 or b == 0
                 or any(seq.max_tokens - seq.num_completion_tokens < k for seq in seqs)):
             return None
         lens = [len(seq) for seq in seqs]
-        pos, slots, ctx_lens = self._draft_step_metadata(seqs, [k] * b, k)
-        pgraph = self._propose_graphs.get(bs)
-        if pgraph is None:
-            pgraph = self._propose_graphs[bs] = ProposeGraph(self, bs, k)
         vgraph = self._verify_graphs.get(bs)
         if vgraph is None:
             vgraph = self._verify_graphs[bs] = VerifyGraph(self, bs, k + 1)
-        tokens = pgraph.run(self._state_rows(seqs), pos, slots, ctx_lens,
-                            [seq.block_table for seq in seqs])
+        tokens = None
+        if pre is not None:
+            graph, ids_before, _, lens_after = pre
+            if graph.bs == bs and ids_before == [seq.seq_id for seq in seqs] and lens_after == lens:
+                tokens = graph.tokens
+                self.prelaunch_stats["used"] += 1
+        if tokens is None:
+            pos, slots, ctx_lens = self._draft_step_metadata(seqs, [k] * b, k)
+            pgraph = self._propose_graphs.get(bs)
+            if pgraph is None:
+                pgraph = self._propose_graphs[bs] = ProposeGraph(self, bs, k)
+            tokens = pgraph.run(self._state_rows(seqs), pos, slots, ctx_lens,
+                                [seq.block_table for seq in seqs])
         if self.draft_override is not None:
             self.draft_override(seqs, tokens)
         if self._proposal_host.numel() < k * bs:
@@ -634,6 +660,16 @@ class ModelRunner:
             state_rows = self._state_rows(seqs)
             cgraph.run([state_rows[i] for i in order])
             self._device_committed = vgraph
+            if prelaunch:
+                chained = self._chained_graphs.get(bs)
+                if chained is None:
+                    chained = self._chained_graphs[bs] = ChainedProposeGraph(self, bs, k, vgraph)
+                vrow = [0] * b
+                for p, i in enumerate(order):
+                    vrow[i] = p
+                chained.launch(state_rows, lens, vrow, [seq.block_table for seq in seqs])
+                self._prelaunched = (chained, [seq.seq_id for seq in seqs], lens, None)
+                self.prelaunch_stats["queued"] += 1
         self._inflight_verify = (order, vgraph, verified, [seqs[i].seq_id for i in range(b)])
         proposed.synchronize()
         table = host.view(k, bs)[:, :b].tolist()
@@ -663,6 +699,11 @@ class ModelRunner:
             out_b[i] = res[t_pad + bs + p]
         self._pending_verify = (vgraph.aux, cu, {seqs[i].seq_id: p for p, i in enumerate(order)})
         self._pending_graph = vgraph
+        if self._prelaunched is not None:
+            # the lengths the queued draft assumed: len + accepted + 1
+            graph, ids_before, lens_before, _ = self._prelaunched
+            self._prelaunched = (graph, ids_before, lens_before,
+                                 [n + a + 1 for n, a in zip(lens_before, out_a)])
         return out_t, out_a, out_b
 
     def _verify_fused(self, seqs: list[Sequence], num_input_tokens: list[int]):

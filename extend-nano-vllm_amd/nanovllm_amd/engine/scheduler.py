@@ -157,6 +157,23 @@ class Scheduler:
         limit = min(seq.max_tokens + seq.num_prompt_tokens, len(seq) + self.num_speculative_tokens)
         self.block_manager.ensure_num_blocks_for_length(seq, limit)
 
+    def reserve_lookahead(self, seqs: list[Sequence]) -> bool:
+        """Pages one step further than reserve_speculation for every
+        sequence (len + 2k tokens, within the token budget), so that the next
+        step's draft can be queued before this step's results are read.
+        False, with nothing reserved, when the pool is short of pages.
+        postprocess_speculation releases what the step does not keep."""
+        bm = self.block_manager
+        k = self.num_speculative_tokens
+        limits = [min(seq.max_tokens + seq.num_prompt_tokens, len(seq) + 2 * k) for seq in seqs]
+        need = sum(max(-(-n // bm.block_size) - len(seq.block_table), 0)
+                   for seq, n in zip(seqs, limits))
+        if need > len(bm.free_block_ids):
+            return False
+        for seq, n in zip(seqs, limits):
+            bm.ensure_num_blocks_for_length(seq, n)
+        return True
+
     def begin_speculation(self, seq: Sequence, proposal_tokens: list[int]) -> int:
         """Append the drafts (their pages are reserved) and return the length
         before them, ``base``."""

@@ -686,6 +686,40 @@ def verify_metadata(start_pos: torch.Tensor, q_lens: torch.Tensor, block_tables:
           "verify_metadata")
 
 
+def draft_metadata(lens: torch.Tensor, verify_row: torch.Tensor, accept_len: torch.Tensor,
+                   num_seqs: int, block_tables: torch.Tensor, block_size: int,
+                   positions: torch.Tensor, slot_mapping: torch.Tensor,
+                   context_lens: torch.Tensor) -> None:
+    """Draft-step metadata after a verify, on the device (the host loop of
+    model_runner.py:1087-1096, :1159-1213): column i < num_seqs of the
+    [steps, bs] outputs is a sequence of length lens[i] +
+    accept_len[verify_row[i]] + 1 after the verified step, its step s at
+    position len - 1 + s (slot through block_tables row i, context + 1);
+    padding columns get position 0, slot -1, context 1.  lens and verify_row
+    are int64 [bs], accept_len int32 (the accept scan's output)."""
+    lib = _native.load()
+    _require_cuda(lens, verify_row, accept_len, block_tables, positions, slot_mapping,
+                  context_lens)
+    if positions.dim() != 2 or positions.dtype != torch.int64 or not positions.is_contiguous():
+        raise ValueError("positions must be contiguous int64 [steps, bs]")
+    steps, bs = positions.shape
+    for t, name in ((slot_mapping, "slot_mapping"), (context_lens, "context_lens")):
+        _i32(t, name)
+        if t.shape != positions.shape or not t.is_contiguous():
+            raise ValueError(f"{name} must be contiguous int32 [steps, bs]")
+    _i32(accept_len, "accept_len")
+    if lens.dtype != torch.int64 or verify_row.dtype != torch.int64 or \
+            lens.numel() < num_seqs or verify_row.numel() < num_seqs:
+        raise ValueError("lens and verify_row must be int64 with an entry per sequence")
+    if not 0 <= num_seqs <= bs:
+        raise ValueError("num_seqs must be within the bs columns")
+    bt_ptr, bt_stride, bt_width = _block_table_args(block_tables, num_seqs)
+    check(lib.nva_draft_metadata(lens.data_ptr(), verify_row.data_ptr(), accept_len.data_ptr(),
+                                 int(num_seqs), bs, steps, bt_ptr, bt_stride, bt_width,
+                                 int(block_size), positions.data_ptr(), slot_mapping.data_ptr(),
+                                 context_lens.data_ptr(), _stream()), "draft_metadata")
+
+
 def commit_metadata(start_pos: torch.Tensor, accept_len: torch.Tensor, q_stride: int,
                     verify_argmax: torch.Tensor, block_tables: torch.Tensor, block_size: int,
                     num_tokens: int, cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor,

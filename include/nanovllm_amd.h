@@ -388,6 +388,25 @@ int nva_commit_metadata(const int32_t *start_pos, const int32_t *accept_len, int
                         int32_t *verify_rows, int64_t *token_ids, int64_t *last_rows,
                         int32_t num_tokens, void *stream);
 
+/* Draft-step metadata for a draft queued right behind a verify, before the
+ *   host has read its results.  Replaces the host loop that builds each
+ *   draft step's position, slot and context length
+ *   (nanovllm/engine/model_runner.py:1087-1096, :1159-1213) for the step
+ *   that follows a verify: sequence i (columns i < num_seqs of bs; the rest
+ *   are padding) has length L_i = lens[i] + accept_len[verify_row[i]] + 1
+ *   after the verified step (accept_len is the accept scan's output, indexed
+ *   by the sequence's row in the verify batch), and its draft step s <
+ *   steps is at position p = L_i - 1 + s: positions[s * bs + i] = p,
+ *   context_lens[...] = p + 1, slot_mapping[...] = block id * block_size +
+ *   p % block_size through block_tables row i (-1 where the block id is
+ *   negative or p is past max_blocks_per_seq pages).  Padding columns get
+ *   position 0, context 1 and slot -1.  Every array is device memory. */
+int nva_draft_metadata(const int64_t *lens, const int64_t *verify_row, const int32_t *accept_len,
+                       int32_t num_seqs, int32_t bs, int32_t steps, const int32_t *block_tables,
+                       int64_t block_table_stride, int32_t max_blocks_per_seq,
+                       int32_t block_size, int64_t *positions, int32_t *slot_mapping,
+                       int32_t *context_lens, void *stream);
+
 /* SiluAndMul (nanovllm/layers/activation.py:11-14): x rows [a | b] of
  *   2*intermediate elements -> out = bf16(bf16(silu(a)) * b). */
 int nva_silu_mul(const void *x, int64_t x_row_stride, void *out, int64_t out_row_stride,

@@ -114,8 +114,8 @@ def test_draft_step_matches_restatement(dirs, eager):
         def recorder(name):
             inner = getattr(runner, name)
 
-            def wrapped(step_seqs):
-                props = inner(step_seqs)
+            def wrapped(step_seqs, *rest):
+                props = inner(step_seqs, *rest)
                 if props is not None:
                     seen.update({s.seq_id: list(p) for s, p in zip(step_seqs, props)})
                 return props

@@ -383,3 +383,64 @@ def test_device_commit_matches_host_commit(dirs):
             torch.testing.assert_close(fa, fb, atol=3e-2, rtol=3e-2)
             compared += 1
     assert compared > 10
+
+
+def test_prelaunched_drafts_equal_fresh_drafts(dirs):
+    """A step's draft queued behind the previous step's verify and device
+    commit (lengths, positions and slots derived on the device from the
+    accept results) proposes exactly what a draft launched after the host's
+    bookkeeping proposes: with acceptance forced by oracle drafts (so the
+    lengths grow by varying amounts), the raw draft tokens of every step,
+    the outputs and the acceptance counts agree between the two engines,
+    and the queued drafts were used."""
+    ps = [prompts(1, seed=31, lo=250, hi=258)[0], prompts(1, seed=32, lo=20, hi=30)[0],
+          prompts(1, seed=33, lo=500, hi=510)[0]]
+    max_tokens = [70, 64, 58]
+    plain = make_llm(dirs, spec=False)
+    try:
+        ref = [plain.generate([p], SamplingParams(temperature=0.0, max_tokens=m, ignore_eos=True),
+                              use_tqdm=False)[0]["token_ids"] for p, m in zip(ps, max_tokens)]
+    finally:
+        plain.exit()
+    full = {tuple(p): p + r for p, r in zip(ps, ref)}
+
+    def run(prelaunch):
+        raw, calls = [], {"n": 0}
+
+        def override(seqs, tokens):
+            k = tokens.shape[0]
+            host = tokens.cpu()
+            raw.append(host[:, :len(seqs)].clone())
+            for i, seq in enumerate(seqs):
+                want = full[tuple(seq.prompt_token_ids)][len(seq):len(seq) + k]
+                calls["n"] += 1
+                for s_, tok in enumerate(want):
+                    host[s_, i] = tok
+                if calls["n"] % 4 == 0:
+                    host[calls["n"] % k, i] = (int(host[calls["n"] % k, i]) + 1) % 2048
+            tokens.copy_(host.to(tokens.device))
+
+        llm = make_llm(dirs, spec=True, k=5, eager=False)
+        llm.prelaunch_draft = prelaunch
+        llm.model_runner.draft_override = override
+        try:
+            for p, m in zip(ps, max_tokens):
+                llm.add_request(p, SamplingParams(temperature=0.0, max_tokens=m, ignore_eos=True))
+            outs = {}
+            while not llm.is_finished():
+                for seq_id, toks in llm.step()[0]:
+                    outs[seq_id] = toks
+            return ([outs[i] for i in sorted(outs)], raw, dict(llm.spec_stats),
+                    dict(llm.model_runner.prelaunch_stats))
+        finally:
+            llm.exit()
+
+    got_on, raw_on, stats_on, pre_on = run(True)
+    got_off, raw_off, stats_off, pre_off = run(False)
+    assert pre_on["used"] >= 5 and pre_on["used"] <= pre_on["queued"], pre_on
+    assert pre_off == {"queued": 0, "used": 0}
+    assert stats_on == stats_off and stats_on["accepted"] > stats_on["steps"]
+    assert got_on == got_off
+    assert len(raw_on) == len(raw_off)
+    for step, (a, b) in enumerate(zip(raw_on, raw_off)):
+        assert torch.equal(a, b), step

@@ -987,3 +987,41 @@ def test_wrappers_refuse_bounds_below_host_lengths(K, cuda):
                                    max_k, 0.1, bt)
     torch.cuda.synchronize()
     assert torch.equal(host.view(torch.int16), dev.view(torch.int16))
+
+
+def test_draft_metadata_after_verify(K, cuda):
+    """nva_draft_metadata: each column's length after the verified step is
+    lens + accept[verify_row] + 1 and its draft steps sit at the positions
+    after it, slots through its block-table row (the host loop of
+    model_runner.py:1087-1096 restated per element); padding columns,
+    positions past the table and negative block ids give slot -1."""
+    g = torch.Generator().manual_seed(51)
+    bs, b, steps, bsz, mb = 16, 11, 4, 32, 6
+    lens = torch.randint(1, bsz * mb - 12, (bs,), generator=g)
+    lens[b:] = 0
+    lens[3] = bsz * mb - 3                       # its later steps run past the table
+    vrow = torch.randperm(bs, generator=g)
+    accept = torch.randint(0, 5, (bs,), generator=g).to(torch.int32)
+    bt = torch.randint(0, 500, (bs, mb), generator=g).to(torch.int32)
+    bt[5, 2] = -1                                # a negative block id
+    bt[b:] = -1
+    pos = torch.zeros(steps, bs, dtype=torch.int64, device=cuda)
+    slots = torch.zeros(steps, bs, dtype=torch.int32, device=cuda)
+    ctx = torch.zeros(steps, bs, dtype=torch.int32, device=cuda)
+    K.draft_metadata(lens.to(cuda), vrow.to(cuda), accept.to(cuda), bs, bt.to(cuda), bsz, pos,
+                     slots, ctx)
+    torch.cuda.synchronize()
+    want_pos = torch.zeros(steps, bs, dtype=torch.int64)
+    want_slot = torch.full((steps, bs), -1, dtype=torch.int32)
+    for i in range(bs):
+        new_len = int(lens[i]) + int(accept[int(vrow[i])]) + 1
+        for s in range(steps):
+            p = new_len - 1 + s
+            want_pos[s, i] = p
+            blk = p // bsz
+            if blk < mb and int(bt[i, blk]) >= 0:
+                want_slot[s, i] = int(bt[i, blk]) * bsz + p % bsz
+    assert torch.equal(pos.cpu(), want_pos)
+    assert torch.equal(slots.cpu(), want_slot)
+    assert torch.equal(ctx.cpu(), (want_pos + 1).to(torch.int32))
+    assert (want_slot[:, 3] == -1).any() and (want_slot[:, b:] == -1).all()
