@@ -852,6 +852,7 @@ def timed_steps(llm, steps: int):
     import torch
 
     before = dict(llm.spec_stats)
+    pre_before = dict(llm.model_runner.prelaunch_stats)
     committed = 0
     torch.cuda.synchronize()
     t0 = time.perf_counter()
@@ -860,7 +861,9 @@ def timed_steps(llm, steps: int):
         committed += -num_tokens
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
-    return elapsed, committed, {k: llm.spec_stats[k] - before[k] for k in before}
+    stats = {k: llm.spec_stats[k] - before[k] for k in before}
+    stats["prelaunch"] = {k: llm.model_runner.prelaunch_stats[k] - pre_before[k] for k in pre_before}
+    return elapsed, committed, stats
 
 
 def reference_steps(llm, steps: int, torch_attention: bool):
@@ -1243,6 +1246,9 @@ def main():
         "committed_tokens": committed,
         "accepted_drafts_per_seq_step": round(stats["accepted"] / max(stats["steps"] * n_active, 1), 4),
         "committed_per_seq_step": round(stats["committed"] / max(stats["steps"] * n_active, 1), 4),
+        "prelaunched_drafts": dict(stats["prelaunch"], note=(
+            "timed steps whose draft was queued behind the previous step's verify "
+            "(used) and next-step drafts queued (queued)")),
         "forced_acceptance": forced,
         "reference_pipeline": ref,
         "reference_pipeline_torch_attention": ref_torch,
