@@ -232,3 +232,41 @@ extern "C" int nva_draft_metadata(const int64_t* lens, const int64_t* verify_row
       max_blocks_per_seq, block_size, positions, slot_mapping, context_lens);
   return launch_status();
 }
+
+// ---------------------------------------------------------------- verify input ids
+
+// One thread per verify row t = p * q + j: row 0 of each sequence is its last
+// committed token, rows 1..q-1 its proposals, read from the draft's output
+// [q-1][proposal_stride] at the sequence's column order[p]; a column outside
+// [0, proposal_stride) marks padding (ids 0), so no read leaves the output.
+// compose[0] == 0 leaves ids as they are (the host wrote them), so one
+// captured graph serves both callers.
+__global__ void __launch_bounds__(kMetaThreads)
+verify_input_ids_kernel(const int32_t* __restrict__ compose, const int32_t* __restrict__ last_tokens,
+                        const int32_t* __restrict__ order, const int64_t* __restrict__ proposals,
+                        int64_t proposal_stride, int32_t num_rows, int32_t q,
+                        int64_t* __restrict__ ids) {
+  const int t = blockIdx.x * kMetaThreads + threadIdx.x;
+  if (t >= num_rows * q || compose[0] == 0) return;
+  const int p = t / q, j = t % q;
+  const int32_t col = order[p];
+  int64_t id = 0;
+  if (col >= 0 && col < proposal_stride)
+    id = j == 0 ? static_cast<int64_t>(last_tokens[p]) : proposals[(j - 1) * proposal_stride + col];
+  ids[t] = id;
+}
+
+extern "C" int nva_verify_input_ids(const int32_t* compose, const int32_t* last_tokens,
+                                    const int32_t* order, const int64_t* proposals,
+                                    int64_t proposal_stride, int32_t num_rows, int32_t q,
+                                    int64_t* ids, void* stream) {
+  if (num_rows < 0 || q < 1 || proposal_stride < 1) return NVA_ERR_ARG;
+  if (num_rows == 0) return NVA_OK;
+  if (!compose || !last_tokens || !order || !ids || (q > 1 && !proposals)) return NVA_ERR_ARG;
+  if (static_cast<int64_t>(num_rows) * q > INT32_MAX) return NVA_ERR_ARG;
+  const int n = num_rows * q;
+  verify_input_ids_kernel<<<(n + kMetaThreads - 1) / kMetaThreads, kMetaThreads, 0,
+                            static_cast<hipStream_t>(stream)>>>(
+      compose, last_tokens, order, proposals, proposal_stride, num_rows, q, ids);
+  return launch_status();
+}

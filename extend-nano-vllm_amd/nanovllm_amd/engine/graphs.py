@@ -144,8 +144,12 @@ class _GraphBase:
 
 class VerifyGraph(_GraphBase):
     """The host uploads per-sequence first positions and query lengths, the
-    block tables and the input ids; positions, slot mapping and cu_seqlens
-    are derived on the device inside the graph (nva_verify_metadata)."""
+    block tables and either the input ids (run) or each sequence's last
+    token and column in the draft's proposals (run_composed: the ids are
+    composed inside the graph, nva_verify_input_ids, from the bucket's
+    proposal buffer that every draft graph writes); positions, slot
+    mapping and cu_seqlens are derived on the device inside the graph
+    (nva_verify_metadata)."""
 
     def __init__(self, runner, bs: int, q: int):
         super().__init__(runner)
@@ -153,8 +157,11 @@ class VerifyGraph(_GraphBase):
         T = self.T
         self.max_blocks = runner.max_blocks_per_seq
         self.i64 = _Staging({"ids": T}, torch.int64, self.device)
-        self.i32 = _Staging({"start": bs, "qlen": bs, "bt": bs * self.max_blocks}, torch.int32,
-                            self.device)
+        self.i32 = _Staging({"compose": 1, "last": bs, "order": bs, "start": bs, "qlen": bs,
+                             "bt": bs * self.max_blocks}, torch.int32, self.device)
+        self.proposals = runner.proposal_buffer(bs)
+        if self.proposals.shape[0] != q - 1:
+            raise ValueError(f"verify rows per sequence ({q}) must be the proposals ({self.proposals.shape[0]}) + 1")
         self.pos = torch.zeros(T, dtype=torch.int64, device=self.device)
         self.slots = torch.zeros(T, dtype=torch.int32, device=self.device)
         self.cu_q = torch.zeros(bs + 1, dtype=torch.int32, device=self.device)
@@ -168,6 +175,9 @@ class VerifyGraph(_GraphBase):
     def _fill_dummy(self):
         bs, q = self.bs, self.q
         self.i64.fill("ids", [0] * self.T)
+        self.i32.fill("compose", [0])
+        self.i32.fill("last", [0] * bs)
+        self.i32.fill("order", [-1] * bs)
         self.i32.fill("start", [0] * bs)
         self.i32.fill("qlen", [q] * bs)
         self.i32.fill("bt", [-1] * (bs * self.max_blocks))
@@ -178,6 +188,8 @@ class VerifyGraph(_GraphBase):
         r = self.runner
         ids = self.i64.dev_view("ids")
         bt = self.i32.dev_view("bt").view(self.bs, self.max_blocks)
+        K.verify_input_ids(self.i32.dev_view("compose"), self.i32.dev_view("last"),
+                           self.i32.dev_view("order"), self.proposals, self.q, ids)
         K.verify_metadata(self.i32.dev_view("start"), self.i32.dev_view("qlen"), bt,
                           r.block_size, self.T, self.cu_q, self.cu_k, self.pos, self.slots)
         set_context(True, self.cu_q, self.cu_k, self.q, r.max_seqlen_k, self.slots, None, bt)
@@ -197,11 +209,24 @@ class VerifyGraph(_GraphBase):
         n = len(ids)
         self.i64.fill("ids", list(ids) + [0] * (self.T - n))
         self.i64.upload()
-        self.run_staged_ids(starts, qlens, bt_rows)
+        self.i32.fill("compose", [0])
+        self._run_staged(starts, qlens, bt_rows)
 
-    def run_staged_ids(self, starts, qlens, bt_rows) -> None:
-        """As run(), with the input ids already in the device view of the
-        ids field (written on the device, e.g. from the draft's proposals)."""
+    def run_composed(self, last_tokens, columns, starts, qlens, bt_rows) -> None:
+        """As run(), for sequences that verify the bucket's proposals in
+        full (q = k + 1 rows each): row p's ids are last_tokens[p] and then
+        the proposals of draft column columns[p], composed inside the graph
+        from whatever the draft graphs last wrote to the proposal buffer."""
+        bs = self.bs
+        b = len(columns)
+        if b > bs or any(not 0 <= c < bs for c in columns) or any(n != self.q for n in qlens):
+            raise ValueError("composed verify rows need draft columns within the bucket and q rows")
+        self.i32.fill("compose", [1])
+        self.i32.fill("last", list(last_tokens) + [0] * (bs - b))
+        self.i32.fill("order", list(columns) + [-1] * (bs - b))
+        self._run_staged(starts, qlens, bt_rows)
+
+    def _run_staged(self, starts, qlens, bt_rows) -> None:
         bs, q = self.bs, self.q
         b = len(starts)
         self.i32.fill("start", list(starts) + [0] * (bs - b))
@@ -222,7 +247,9 @@ class ProposeGraph(_GraphBase):
         steps = max(k - 1, 1)
         self.hidden = torch.zeros(bs, h, dtype=r.dtype, device=self.device)
         self.feedback = torch.zeros(bs, h, dtype=r.dtype, device=self.device)
-        self.tokens = torch.zeros(k, bs, dtype=torch.int64, device=self.device)
+        self.tokens = r.proposal_buffer(bs)
+        if self.tokens.shape[0] != k:
+            raise ValueError(f"draft steps ({k}) must match the proposal buffer ({self.tokens.shape[0]})")
         # the draft-state rows of the batch (gathered inside the graph) and
         # the draft steps' metadata, one host->device copy per dtype
         self.i64 = _Staging({"state": bs, "pos": steps * bs}, torch.int64, self.device)

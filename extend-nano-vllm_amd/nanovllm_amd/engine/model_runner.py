@@ -100,6 +100,7 @@ class ModelRunner:
             self._commit_graphs: dict[tuple[int, int], CommitGraph] = {}
             self._device_commit_graphs: dict[int, DeviceCommitGraph] = {}
             self._chained_graphs: dict[int, ChainedProposeGraph] = {}
+            self._proposal_buffers: dict[int, torch.Tensor] = {}
             self._device_committed = None
             self._pending_verify = None
             self._pending_graph = None
@@ -167,6 +168,17 @@ class ModelRunner:
         return {sid: Eagle3KVCache(self.state_hidden[r:r + 1], self.state_feedback[r:r + 1])
                 for sid, r in self._state_slot.items()}
 
+    def proposal_buffer(self, bs: int) -> torch.Tensor:
+        """The [k, bs] int64 proposals of bucket bs: every draft graph of the
+        bucket writes its tokens here and the bucket's verify graph composes
+        its input ids from here, so the captured graphs share one address."""
+        buf = self._proposal_buffers.get(bs)
+        if buf is None:
+            k = self.speculative_config.num_speculative_tokens
+            buf = self._proposal_buffers[bs] = torch.zeros(k, bs, dtype=torch.int64,
+                                                           device=self.device)
+        return buf
+
     def _state_rows(self, seqs) -> list[int]:
         rows = []
         for seq in seqs:
@@ -199,6 +211,7 @@ class ModelRunner:
         self._verify_graphs.clear()
         self._propose_graphs.clear()
         self._chained_graphs.clear()
+        self._proposal_buffers.clear()
         self._prelaunched = None
         self._inflight_verify = None
         self._device_committed = None
@@ -632,20 +645,13 @@ class ModelRunner:
         host.copy_(tokens.reshape(-1), non_blocking=True)
         proposed = torch.cuda.Event()
         proposed.record()
-        # the verify batch runs longest sequence first (verify_eagle3_batch_fused)
+        # the verify batch runs longest sequence first (verify_eagle3_batch_fused);
+        # its input ids are composed inside the graph from the proposals
         order = sorted(range(b), key=lambda i: -lens[i])
-        order_d = _pinned(order, torch.int64).to(self.device, non_blocking=True)
-        last_d = _pinned([seqs[i].token_ids[-1] for i in order], torch.int64).to(
-            self.device, non_blocking=True)
         q = k + 1
-        ids = vgraph.i64.dev_view("ids")
-        rows = ids[:b * q].view(b, q)
-        rows[:, 0].copy_(last_d)
-        rows[:, 1:].copy_(tokens[:, :b].index_select(1, order_d).t())
-        if b * q < ids.numel():
-            ids[b * q:].zero_()
-        vgraph.run_staged_ids([lens[i] - 1 for i in order], [q] * b,
-                              [seqs[i].block_table for i in order])
+        vgraph.run_composed([seqs[i].token_ids[-1] for i in order], order,
+                            [lens[i] - 1 for i in order], [q] * b,
+                            [seqs[i].block_table for i in order])
         t_pad = vgraph.T
         self._verify_host[:t_pad + 2 * bs].copy_(vgraph.out, non_blocking=True)
         verified = torch.cuda.Event()

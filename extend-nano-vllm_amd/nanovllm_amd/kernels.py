@@ -720,6 +720,32 @@ def draft_metadata(lens: torch.Tensor, verify_row: torch.Tensor, accept_len: tor
                                  context_lens.data_ptr(), _stream()), "draft_metadata")
 
 
+
+def verify_input_ids(compose: torch.Tensor, last_tokens: torch.Tensor, order: torch.Tensor,
+                     proposals: torch.Tensor, q: int, ids: torch.Tensor) -> None:
+    """The verify batch's input ids on the device (each sequence's last
+    token, then its proposals: llm_engine.py:129-141 with
+    model_runner.py:770-774): row p of q ids is last_tokens[p] followed by
+    proposals[:, order[p]] (proposals [q-1, stride] int64, the draft's
+    output); rows whose order[p] is outside [0, stride) are padding (ids 0).
+    compose, last_tokens and order are int32 device tensors; when
+    compose[0] == 0 the kernel leaves ids untouched."""
+    lib = _native.load()
+    _require_cuda(compose, last_tokens, order, proposals, ids)
+    for t, name in ((compose, "compose"), (last_tokens, "last_tokens"), (order, "order")):
+        _i32(t, name)
+    num_rows = order.numel()
+    if last_tokens.numel() != num_rows or compose.numel() < 1:
+        raise ValueError("last_tokens needs an entry per row and compose one flag")
+    if proposals.dim() != 2 or proposals.dtype != torch.int64 or not proposals.is_contiguous() \
+            or proposals.shape[0] < q - 1 or proposals.shape[1] < 1:
+        raise ValueError("proposals must be contiguous int64 [q-1, stride]")
+    if ids.dtype != torch.int64 or not ids.is_contiguous() or ids.numel() < num_rows * q:
+        raise ValueError("ids must be contiguous int64 with num_rows * q entries")
+    check(lib.nva_verify_input_ids(compose.data_ptr(), last_tokens.data_ptr(), order.data_ptr(),
+                                   proposals.data_ptr(), proposals.shape[1], num_rows, int(q),
+                                   ids.data_ptr(), _stream()), "verify_input_ids")
+
 def commit_metadata(start_pos: torch.Tensor, accept_len: torch.Tensor, q_stride: int,
                     verify_argmax: torch.Tensor, block_tables: torch.Tensor, block_size: int,
                     num_tokens: int, cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor,

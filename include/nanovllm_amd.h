@@ -407,6 +407,23 @@ int nva_draft_metadata(const int64_t *lens, const int64_t *verify_row, const int
                        int32_t block_size, int64_t *positions, int32_t *slot_mapping,
                        int32_t *context_lens, void *stream);
 
+/* Verify input ids composed on the device from the draft's proposals.
+ *   Replaces the reference's verify input, each sequence's last
+ *   num_scheduled_tokens tokens after its proposals were appended
+ *   (nanovllm/engine/llm_engine.py:129-141 appends them,
+ *   nanovllm/engine/model_runner.py:770-774 reads them): for verify row
+ *   t = p * q + j of sequence p (num_rows sequences of q rows),
+ *   ids[t] = last_tokens[p] for j == 0 and
+ *   proposals[(j - 1) * proposal_stride + order[p]] for j >= 1, the draft's
+ *   output laid out [q-1][proposal_stride] with the sequence in column
+ *   order[p].  A row whose order[p] is outside [0, proposal_stride) is
+ *   padding: its q ids are 0.  When compose[0] == 0 nothing is written
+ *   (ids keep what the host uploaded), so a captured graph can hold the
+ *   launch for both uses.  Every array is device memory. */
+int nva_verify_input_ids(const int32_t *compose, const int32_t *last_tokens, const int32_t *order,
+                         const int64_t *proposals, int64_t proposal_stride, int32_t num_rows,
+                         int32_t q, int64_t *ids, void *stream);
+
 /* SiluAndMul (nanovllm/layers/activation.py:11-14): x rows [a | b] of
  *   2*intermediate elements -> out = bf16(bf16(silu(a)) * b). */
 int nva_silu_mul(const void *x, int64_t x_row_stride, void *out, int64_t out_row_stride,

@@ -989,6 +989,40 @@ def test_wrappers_refuse_bounds_below_host_lengths(K, cuda):
     assert torch.equal(host.view(torch.int16), dev.view(torch.int16))
 
 
+def test_verify_input_ids_from_proposals(K, cuda):
+    """nva_verify_input_ids against the reference's own route to the verify
+    input: each sequence's proposals appended to its tokens
+    (llm_engine.py:129-141), then its last k + 1 tokens read from
+    num_computed_tokens = len - 1 (model_runner.py:770-774); rows in the
+    longest-first verify order, padding rows 0, and compose = 0 leaving the
+    host's ids in place."""
+    g = torch.Generator().manual_seed(53)
+    bs, b, k = 16, 11, 5
+    q = k + 1
+    seqs = [torch.randint(0, 151936, (int(n),), generator=g).tolist()
+            for n in torch.randint(1, 40, (b,), generator=g)]
+    props = torch.randint(0, 151936, (k, bs), generator=g)
+    order = sorted(range(b), key=lambda i: -len(seqs[i]))
+    want = []
+    for i in order:
+        tokens = seqs[i] + props[:, i].tolist()
+        start = len(seqs[i]) - 1
+        want += tokens[start:start + q]
+    want += [0] * ((bs - b) * q)
+    compose = torch.ones(1, dtype=torch.int32, device=cuda)
+    last = torch.tensor([seqs[i][-1] for i in order] + [0] * (bs - b), dtype=torch.int32)
+    cols = torch.tensor(order + [-1] * (bs - b - 1) + [bs], dtype=torch.int32)  # bs: out of range
+    ids = torch.full((bs * q,), 7, dtype=torch.int64, device=cuda)
+    K.verify_input_ids(compose, last.to(cuda), cols.to(cuda), props.to(cuda), q, ids)
+    torch.cuda.synchronize()
+    assert ids.cpu().tolist() == want
+    compose.zero_()
+    host = torch.arange(bs * q, dtype=torch.int64, device=cuda)
+    K.verify_input_ids(compose, last.to(cuda), cols.to(cuda), props.to(cuda), q, host)
+    torch.cuda.synchronize()
+    assert torch.equal(host.cpu(), torch.arange(bs * q))
+
+
 def test_draft_metadata_after_verify(K, cuda):
     """nva_draft_metadata: each column's length after the verified step is
     lens + accept[verify_row] + 1 and its draft steps sit at the positions
