@@ -21,12 +21,14 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t b) {
 }
 
 // Round-to-nearest-even float -> bf16, NaN -> 0x7FC0 (the conversion torch
-// applies when it stores a float result as bfloat16).
+// applies when it stores a float result as bfloat16).  gfx950's
+// v_cvt_pk_bf16_f32 rounds to nearest even, subnormals included (the
+// kernels run with f32 denormals preserved); only a NaN's payload differs
+// from torch's, hence the select.  Three instructions against the integer
+// rounding's seven.
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0;
-  uint32_t bias = ((u >> 16) & 1u) + 0x7FFFu;
-  return static_cast<uint16_t>((u + bias) >> 16);
+  const uint16_t r = __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
+  return f != f ? static_cast<uint16_t>(0x7FC0) : r;
 }
 
 // ---------------------------------------------------------------- fp8 e4m3fn

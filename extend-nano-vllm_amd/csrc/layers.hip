@@ -305,23 +305,15 @@ qk_norm_rope_store_kernel(const uint16_t* __restrict__ qkv, int64_t row_stride,
   }
 }
 
-// float -> bf16 by gfx950's v_cvt_pk_bf16_f32 (round to nearest even, as
-// f32_to_bf16; a NaN stays a quiet NaN but keeps its payload's top bits
-// instead of becoming 0x7FC0).  One instruction against f32_to_bf16's five.
-__device__ __forceinline__ uint16_t f32_to_bf16_cvt(float f) {
-  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
-}
-
 // out = bf16( bf16(silu(a)) * b ) for a row [a | b] (activation.py:11-14:
 // F.silu in bf16, then a bf16 product).  The division stays IEEE: with the
 // hardware reciprocal in its place silu(a)'s bf16 rounding flips next to
 // rounding midpoints, and the product's second rounding then leaves the
-// one-ulp bound against torch.  The two bf16 roundings are one instruction
-// each (about 21 instructions an element against 30).
+// one-ulp bound against torch.
 __device__ __forceinline__ uint16_t silu_mul_one(uint16_t a, uint16_t b) {
   const float av = bf16_to_f32(a);
-  const float sv = bf16_to_f32(f32_to_bf16_cvt(av / (1.0f + __expf(-av))));
-  return f32_to_bf16_cvt(sv * bf16_to_f32(b));
+  const float sv = bf16_to_f32(f32_to_bf16(av / (1.0f + __expf(-av))));
+  return f32_to_bf16(sv * bf16_to_f32(b));
 }
 
 // vec: 16-byte vectors of 8 elements (rows and strides multiples of 8,
