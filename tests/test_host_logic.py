@@ -122,6 +122,79 @@ def test_rejection_frees_the_reserved_page():
     _check_invariants(sched, [seq])
 
 
+def test_reserve_lookahead_takes_two_steps_of_pages():
+    """Scheduler.reserve_lookahead: pages for len + 2k tokens (the next
+    step's draft is queued before this step's results are read), capped by
+    the token budget; what the step does not keep goes back in
+    postprocess_speculation."""
+    sched = _scheduler(num_blocks=4)
+    seq = Sequence(list(range(250)), SamplingParams(temperature=0.0, max_tokens=64,
+                                                    ignore_eos=True))
+    capped = Sequence(list(range(500, 750)), SamplingParams(temperature=0.0, max_tokens=3,
+                                                            ignore_eos=True))
+    sched.add(seq)
+    sched.add(capped)
+    seqs, is_prefill = sched.schedule()
+    assert is_prefill and seqs == [seq, capped]
+    sched.postprocess(seqs, [1, 2], True)
+    seqs, is_prefill = sched.schedule()
+    assert not is_prefill and seqs == [seq, capped]
+    sched.reserve_speculation(seq)
+    assert len(seq) == 251 and len(seq.block_table) == 1      # 251 + 5 tokens
+    assert sched.reserve_lookahead([seq, capped])
+    assert len(seq.block_table) == 2                          # 251 + 10 tokens
+    assert len(capped.block_table) == 1                       # budget: 250 + 3 tokens
+    free = len(sched.block_manager.free_block_ids)
+    base = sched.begin_speculation(seq, [5, 6, 7, 8, 9])
+    seq.num_computed_tokens = base - 1
+    v = verify_greedy_proposals([5, 6, 7, 8, 9], [4, 6, 7, 8, 9, 10])
+    assert sched.postprocess_speculation(seq, base, v.accepted_tokens, v.replacement_token) == 0
+    assert len(seq) == 252 and len(seq.block_table) == 1      # the look-ahead page went back
+    assert len(sched.block_manager.free_block_ids) == free + 1
+    _check_invariants(sched, [seq, capped])
+
+
+def test_reserve_lookahead_is_all_or_nothing():
+    """Short of pages for every sequence's look-ahead, nothing is reserved."""
+    sched = _scheduler(num_blocks=3)
+    a = Sequence(list(range(250)), SamplingParams(temperature=0.0, max_tokens=64, ignore_eos=True))
+    b = Sequence(list(range(300, 550)), SamplingParams(temperature=0.0, max_tokens=64,
+                                                       ignore_eos=True))
+    sched.add(a)
+    sched.add(b)
+    seqs, is_prefill = sched.schedule()
+    assert is_prefill and seqs == [a, b]
+    sched.postprocess(seqs, [1, 2], True)
+    assert len(a.block_table) == len(b.block_table) == 1
+    free = list(sched.block_manager.free_block_ids)
+    assert len(free) == 1                                  # each needs a second page
+    assert not sched.reserve_lookahead([a, b])
+    assert len(a.block_table) == len(b.block_table) == 1
+    assert list(sched.block_manager.free_block_ids) == free
+    assert sched.reserve_lookahead([a])
+    bm = sched.block_manager
+    assert len(a.block_table) == 2 and not bm.free_block_ids
+    # mid-step a holds one page beyond its length; the pool still adds up
+    assert bm.used_block_ids == set(a.block_table) | set(b.block_table)
+    assert len(bm.used_block_ids) == len(bm.blocks)
+
+
+def test_block_table_array_pads_rows_and_rejects_wide_ones():
+    """The graphs' block-table staging: rows padded with -1 to the width,
+    -1 rows past the given ones, the rows' lengths returned; a row wider
+    than the width is an error, not a silent clip."""
+    from nanovllm_amd.engine.graphs import block_table_array
+    out, lens = block_table_array([[4, 9], [7], []], nrows=4, width=3)
+    assert out.dtype.name == "int32" and out.tolist() == [[4, 9, -1], [7, -1, -1],
+                                                          [-1, -1, -1], [-1, -1, -1]]
+    assert lens.tolist() == [2, 1, 0]
+    out, _ = block_table_array([[1, 2, 3], [5]])
+    assert out.tolist() == [[1, 2, 3], [5, -1, -1]]
+    assert block_table_array([])[0].shape == (0, 1)
+    with pytest.raises(ValueError):
+        block_table_array([[1, 2, 3]], nrows=1, width=2)
+
+
 def test_eos_inside_accepted_drafts_ends_the_sequence():
     """EOS truncation drops the replacement and finishes (scheduler.py:158-163)."""
     sched = _scheduler(eos=7)
