@@ -686,12 +686,14 @@ def test_qk_norm_rope_store_matches_separate_kernels(K, cuda, layout, fp8, with_
     assert changed.any()
 
 
-def test_silu_mul_vector_path_matches_scalar_and_reference(K, cuda):
+@pytest.mark.parametrize("inter", [1000, 4104])
+def test_silu_mul_vector_path_matches_scalar_and_reference(K, cuda, inter):
     """16-byte vector path == element path (bit-exact); both within one bf16
     ulp of torch's bf16(bf16(silu(a)) * b) (activation.py:11-14), whose exp
-    may round differently from the device's."""
+    may round differently from the device's.  4104 = 513 vectors a row: the
+    row's last block holds a single vector."""
     g = torch.Generator().manual_seed(41)
-    rows, inter = 40, 1000
+    rows = 40
     full = (torch.randn(rows, 2 * inter + 1, generator=g) * 3).to(torch.bfloat16).to(cuda)
     x_vec = full[:, :2 * inter].contiguous()           # row stride 2000: vector path
     x_scalar = full[:, :2 * inter]                      # row stride 2001: element path
