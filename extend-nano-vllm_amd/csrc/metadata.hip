@@ -16,6 +16,15 @@
 // and each commit row also gets its verify row, its token (the verify
 // argmax of that row, which an accepted draft equals) and each sequence its
 // last commit row, whose draft states seed the next proposal.
+//
+// Draft slot convention.  The draft forms (commit and draft steps) take a
+// slot offset: the K/V of RoPE position p goes to the slot of position
+// p + slot_offset, and that row sees p + slot_offset + 1 keys.  Offset 0
+// stores position p at slot p, as the reference's draft prefill does
+// (model_runner.py:1379-1390); offset 1 is the reference's decode and
+// commit convention (slot len + step, context len + step + 1,
+// model_runner.py:1087-1096; slot start + 1 + i, context start + 2 + i,
+// :1143-1149).
 #include "common.h"
 
 namespace nva {
@@ -57,9 +66,9 @@ __global__ void __launch_bounds__(kMetaThreads)
 verify_metadata_kernel(const int32_t* __restrict__ start_pos, const int32_t* __restrict__ q_lens,
                        int32_t num_seqs, const int32_t* __restrict__ block_tables,
                        int64_t bt_stride, int32_t max_blocks, int32_t block_size,
-                       int32_t* __restrict__ cu_q_out, int32_t* __restrict__ cu_k_out,
-                       int64_t* __restrict__ positions, int32_t* __restrict__ slots,
-                       int32_t num_tokens, CommitArgs ca) {
+                       int32_t slot_offset, int32_t* __restrict__ cu_q_out,
+                       int32_t* __restrict__ cu_k_out, int64_t* __restrict__ positions,
+                       int32_t* __restrict__ slots, int32_t num_tokens, CommitArgs ca) {
   __shared__ int cu_q[kMaxMetaSeqs + 1];
   __shared__ int cu_k[kMaxMetaSeqs + 1];
   __shared__ int scan[kMetaThreads];
@@ -79,7 +88,7 @@ verify_metadata_kernel(const int32_t* __restrict__ start_pos, const int32_t* __r
       q = (q < 0 ? 0 : q) + 1;
       q = q < ca.q_stride ? q : ca.q_stride;
     }
-    const int k = i < num_seqs ? start_pos[i] + q : 0;
+    const int k = i < num_seqs ? start_pos[i] + q + slot_offset : 0;
     const int iq = block_scan(q, scan) + carry_q;
     const int ik = block_scan(k, scan) + carry_k;
     if (i < num_seqs) {
@@ -111,10 +120,11 @@ verify_metadata_kernel(const int32_t* __restrict__ start_pos, const int32_t* __r
       }
       const int p = start_pos[lo] + (t - cu_q[lo]);
       pos = p;
-      const int b = p / block_size;
-      if (p >= 0 && b < max_blocks) {
+      const int ps = p + slot_offset;      // the position whose slot holds p's K/V
+      const int b = ps / block_size;
+      if (ps >= 0 && b < max_blocks) {
         const int32_t id = block_tables[static_cast<int64_t>(lo) * bt_stride + b];
-        if (id >= 0) slot = id * block_size + p % block_size;
+        if (id >= 0) slot = id * block_size + ps % block_size;
       }
       if (COMMIT) vrow = lo * ca.q_stride + (t - cu_q[lo]);
     }
@@ -149,7 +159,7 @@ extern "C" int nva_verify_metadata(const int32_t* start_pos, const int32_t* q_le
     return NVA_ERR_ARG;
   verify_metadata_kernel<false><<<1, kMetaThreads, 0, static_cast<hipStream_t>(stream)>>>(
       start_pos, q_lens, num_seqs, block_tables, block_table_stride, max_blocks_per_seq, block_size,
-      cu_seqlens_q, cu_seqlens_k, positions, slot_mapping, num_tokens, CommitArgs{});
+      0, cu_seqlens_q, cu_seqlens_k, positions, slot_mapping, num_tokens, CommitArgs{});
   return launch_status();
 }
 
@@ -158,12 +168,12 @@ extern "C" int nva_commit_metadata(const int32_t* start_pos, const int32_t* acce
                                    const int32_t* verify_argmax, int32_t num_verify_rows,
                                    const int32_t* block_tables, int64_t block_table_stride,
                                    int32_t max_blocks_per_seq, int32_t block_size,
-                                   int32_t* cu_seqlens_q, int32_t* cu_seqlens_k,
-                                   int64_t* positions, int32_t* slot_mapping,
-                                   int32_t* verify_rows, int64_t* token_ids, int64_t* last_rows,
-                                   int32_t num_tokens, void* stream) {
+                                   int32_t slot_offset, int32_t* cu_seqlens_q,
+                                   int32_t* cu_seqlens_k, int64_t* positions,
+                                   int32_t* slot_mapping, int32_t* verify_rows, int64_t* token_ids,
+                                   int64_t* last_rows, int32_t num_tokens, void* stream) {
   if (num_seqs < 0 || num_tokens < 0 || block_size <= 0 || max_blocks_per_seq < 0 ||
-      q_stride <= 0 || num_verify_rows < 0)
+      q_stride <= 0 || num_verify_rows < 0 || (slot_offset != 0 && slot_offset != 1))
     return NVA_ERR_ARG;
   if (num_seqs > kMaxMetaSeqs) return NVA_ERR_UNSUPPORTED;
   if (block_table_stride < max_blocks_per_seq) return NVA_ERR_ARG;
@@ -177,7 +187,7 @@ extern "C" int nva_commit_metadata(const int32_t* start_pos, const int32_t* acce
   const CommitArgs ca{q_stride, verify_argmax, num_verify_rows, verify_rows, token_ids, last_rows};
   verify_metadata_kernel<true><<<1, kMetaThreads, 0, static_cast<hipStream_t>(stream)>>>(
       start_pos, accept_len, num_seqs, block_tables, block_table_stride, max_blocks_per_seq,
-      block_size, cu_seqlens_q, cu_seqlens_k, positions, slot_mapping, num_tokens, ca);
+      block_size, slot_offset, cu_seqlens_q, cu_seqlens_k, positions, slot_mapping, num_tokens, ca);
   return launch_status();
 }
 
@@ -185,40 +195,45 @@ extern "C" int nva_commit_metadata(const int32_t* start_pos, const int32_t* acce
 // bs (i < num_seqs a sequence, the rest padding), row s of steps.  One
 // thread per (s, i); each reads its sequence's accepted count from the
 // verify's accept output, so the draft's lengths follow the verified step
-// without the host.
+// without the host.  Step s of a sequence of length L is at RoPE position
+// p = L - 1 + s; its K/V go to the slot of position p + slot_offset and it
+// sees p + slot_offset + 1 keys.
 __global__ void __launch_bounds__(kMetaThreads)
 draft_metadata_kernel(const int64_t* __restrict__ lens, const int64_t* __restrict__ verify_row,
                       const int32_t* __restrict__ accept_len, int32_t num_seqs, int32_t bs,
                       int32_t steps, const int32_t* __restrict__ block_tables,
                       int64_t bt_stride, int32_t max_blocks, int32_t block_size,
-                      int64_t* __restrict__ positions, int32_t* __restrict__ slot_mapping,
-                      int32_t* __restrict__ context_lens) {
+                      int32_t slot_offset, int64_t* __restrict__ positions,
+                      int32_t* __restrict__ slot_mapping, int32_t* __restrict__ context_lens) {
   const int idx = blockIdx.x * kMetaThreads + threadIdx.x;
   if (idx >= steps * bs) return;
   const int s = idx / bs, i = idx % bs;
   int64_t pos = 0;
   int32_t slot = -1;
+  int32_t keys = 1;
   if (i < num_seqs) {
     const int64_t len = lens[i] + accept_len[verify_row[i]] + 1;
     pos = len - 1 + s;
-    const int64_t blk = pos / block_size;
-    const int32_t id = pos >= 0 && blk < max_blocks
+    const int64_t ps = pos + slot_offset;   // the position whose slot holds pos's K/V
+    const int64_t blk = ps / block_size;
+    const int32_t id = ps >= 0 && blk < max_blocks
                            ? block_tables[static_cast<int64_t>(i) * bt_stride + blk] : -1;
-    if (id >= 0) slot = static_cast<int32_t>(static_cast<int64_t>(id) * block_size + pos % block_size);
+    if (id >= 0) slot = static_cast<int32_t>(static_cast<int64_t>(id) * block_size + ps % block_size);
+    keys = static_cast<int32_t>(ps + 1);
   }
   positions[idx] = pos;
   slot_mapping[idx] = slot;
-  context_lens[idx] = static_cast<int32_t>(pos + 1);
+  context_lens[idx] = keys;
 }
 
 extern "C" int nva_draft_metadata(const int64_t* lens, const int64_t* verify_row,
                                   const int32_t* accept_len, int32_t num_seqs, int32_t bs,
                                   int32_t steps, const int32_t* block_tables,
                                   int64_t block_table_stride, int32_t max_blocks_per_seq,
-                                  int32_t block_size, int64_t* positions, int32_t* slot_mapping,
-                                  int32_t* context_lens, void* stream) {
+                                  int32_t block_size, int32_t slot_offset, int64_t* positions,
+                                  int32_t* slot_mapping, int32_t* context_lens, void* stream) {
   if (num_seqs < 0 || bs < num_seqs || steps < 0 || block_size <= 0 || max_blocks_per_seq < 0 ||
-      block_table_stride < max_blocks_per_seq)
+      block_table_stride < max_blocks_per_seq || (slot_offset != 0 && slot_offset != 1))
     return NVA_ERR_ARG;
   if (steps == 0 || bs == 0) return NVA_OK;
   if (!positions || !slot_mapping || !context_lens) return NVA_ERR_ARG;
@@ -229,7 +244,7 @@ extern "C" int nva_draft_metadata(const int64_t* lens, const int64_t* verify_row
   draft_metadata_kernel<<<(n + kMetaThreads - 1) / kMetaThreads, kMetaThreads, 0,
                           static_cast<hipStream_t>(stream)>>>(
       lens, verify_row, accept_len, num_seqs, bs, steps, block_tables, block_table_stride,
-      max_blocks_per_seq, block_size, positions, slot_mapping, context_lens);
+      max_blocks_per_seq, block_size, slot_offset, positions, slot_mapping, context_lens);
   return launch_status();
 }
 

@@ -64,11 +64,11 @@ SIGNATURES = {
                                       _P, _P, _P]),
     "nva_silu_mul": (_INT, [_P, _I64, _P, _I64, _I32, _I32, _P]),
     "nva_verify_metadata": (_INT, [_P, _P, _I32, _P, _I64, _I32, _I32, _P, _P, _P, _P, _I32, _P]),
-    "nva_draft_metadata": (_INT, [_P, _P, _P, _I32, _I32, _I32, _P, _I64, _I32, _I32, _P, _P, _P,
-                                  _P]),
+    "nva_draft_metadata": (_INT, [_P, _P, _P, _I32, _I32, _I32, _P, _I64, _I32, _I32, _I32, _P,
+                                  _P, _P, _P]),
     "nva_verify_input_ids": (_INT, [_P, _P, _P, _P, _I64, _I32, _I32, _P, _P]),
-    "nva_commit_metadata": (_INT, [_P, _P, _I32, _I32, _P, _I32, _P, _I64, _I32, _I32, _P, _P, _P,
-                                   _P, _P, _P, _P, _I32, _P]),
+    "nva_commit_metadata": (_INT, [_P, _P, _I32, _I32, _P, _I32, _P, _I64, _I32, _I32, _I32, _P,
+                                   _P, _P, _P, _P, _P, _P, _I32, _P]),
 }
 
 

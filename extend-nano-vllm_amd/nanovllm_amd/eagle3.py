@@ -210,15 +210,6 @@ class Eagle3ForCausalLM(nn.Module):
         return self.forward_with_cache(input_ids, positions,
                                        self.combine_hidden_states(target_hidden_states))[0]
 
-    def compute_logits(self, hidden_states, map_to_target_vocab: bool = False):
-        logits = F.linear(hidden_states, self.lm_head.weight)
-        if not map_to_target_vocab:
-            return logits
-        idx = torch.arange(self.config.draft_vocab_size, device=logits.device) + self.d2t
-        mapped = logits.new_full((logits.size(0), self.config.target_vocab_size), float("-inf"))
-        mapped[:, idx] = logits
-        return mapped
-
     def sample_greedy(self, hidden_states: torch.Tensor, out: torch.Tensor | None = None):
         """argmax of the draft logits mapped to target ids (eagle3.py:294-296),
         fused in the argmax kernel."""

@@ -66,7 +66,16 @@ def block_table_array(rows, nrows: int | None = None,
 
 class _Staging:
     """A device buffer plus a pinned host twin of the same dtype; fields are
-    contiguous slices of both."""
+    contiguous slices of both.
+
+    upload() only queues the copy: the DMA reads the pinned buffer when the
+    stream reaches it, which for the graphs queued behind a verify (the
+    device commit, the next step's draft) can be after the host has started
+    the next step.  So upload() records an event behind its copy, and the
+    first fill() after it waits for that event before writing: a queued
+    copy never reads values meant for the next one.  The wait precedes
+    waits the host makes anyway (each step reads the proposals that the
+    queued graphs produce after their copies), so it costs no step time."""
 
     def __init__(self, sizes: dict[str, int], dtype: torch.dtype, device: torch.device):
         total = sum(sizes.values())
@@ -82,20 +91,34 @@ class _Staging:
             self.fields[name] = (off, n)
             off += n
         self.total = total
+        self._copied = torch.cuda.Event()
+        self._in_flight = False
+        self.waits = 0      # fills that found the previous copy still queued
 
     def dev_view(self, name: str) -> torch.Tensor:
         off, n = self.fields[name]
         return self.dev[off:off + n]
+
+    def _writable(self) -> None:
+        if self._in_flight:
+            if not self._copied.query():
+                self.waits += 1
+                self._copied.synchronize()
+            self._in_flight = False
 
     def fill(self, name: str, values) -> None:
         off, n = self.fields[name]
         a = np.asarray(values, dtype=self.host_np.dtype).reshape(-1)
         if a.size != n:
             raise ValueError(f"{name}: {a.size} values for {n} slots")
+        self._writable()
         self.host_np[off:off + n] = a
 
     def upload(self) -> None:
+        self._writable()
         self.dev[:self.total].copy_(self.host[:self.total], non_blocking=True)
+        self._copied.record()
+        self._in_flight = True
 
 
 class _GraphBase:

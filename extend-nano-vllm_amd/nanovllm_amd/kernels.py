@@ -689,14 +689,18 @@ def verify_metadata(start_pos: torch.Tensor, q_lens: torch.Tensor, block_tables:
 def draft_metadata(lens: torch.Tensor, verify_row: torch.Tensor, accept_len: torch.Tensor,
                    num_seqs: int, block_tables: torch.Tensor, block_size: int,
                    positions: torch.Tensor, slot_mapping: torch.Tensor,
-                   context_lens: torch.Tensor) -> None:
+                   context_lens: torch.Tensor, slot_offset: int = 0) -> None:
     """Draft-step metadata after a verify, on the device (the host loop of
     model_runner.py:1087-1096, :1159-1213): column i < num_seqs of the
     [steps, bs] outputs is a sequence of length lens[i] +
     accept_len[verify_row[i]] + 1 after the verified step, its step s at
-    position len - 1 + s (slot through block_tables row i, context + 1);
-    padding columns get position 0, slot -1, context 1.  lens and verify_row
-    are int64 [bs], accept_len int32 (the accept scan's output)."""
+    RoPE position p = len - 1 + s, its K/V at the slot of position
+    p + slot_offset (through block_tables row i) and its context
+    p + slot_offset + 1; padding columns get position 0, slot -1, context 1.
+    slot_offset 1 is the reference's decode convention (slot len + step,
+    context len + step + 1), 0 this engine's (slot p, context p + 1).  lens
+    and verify_row are int64 [bs], accept_len int32 (the accept scan's
+    output)."""
     lib = _native.load()
     _require_cuda(lens, verify_row, accept_len, block_tables, positions, slot_mapping,
                   context_lens)
@@ -716,8 +720,9 @@ def draft_metadata(lens: torch.Tensor, verify_row: torch.Tensor, accept_len: tor
     bt_ptr, bt_stride, bt_width = _block_table_args(block_tables, num_seqs)
     check(lib.nva_draft_metadata(lens.data_ptr(), verify_row.data_ptr(), accept_len.data_ptr(),
                                  int(num_seqs), bs, steps, bt_ptr, bt_stride, bt_width,
-                                 int(block_size), positions.data_ptr(), slot_mapping.data_ptr(),
-                                 context_lens.data_ptr(), _stream()), "draft_metadata")
+                                 int(block_size), int(slot_offset), positions.data_ptr(),
+                                 slot_mapping.data_ptr(), context_lens.data_ptr(), _stream()),
+          "draft_metadata")
 
 
 
@@ -751,7 +756,7 @@ def commit_metadata(start_pos: torch.Tensor, accept_len: torch.Tensor, q_stride:
                     num_tokens: int, cu_seqlens_q: torch.Tensor, cu_seqlens_k: torch.Tensor,
                     positions: torch.Tensor, slot_mapping: torch.Tensor,
                     verify_rows: torch.Tensor, token_ids: torch.Tensor,
-                    last_rows: torch.Tensor) -> None:
+                    last_rows: torch.Tensor, slot_offset: int = 0) -> None:
     """Device-side metadata of the draft's replay of the committed tails
     (commit_eagle3, model_runner.py:1216-1249): sequence i commits
     accept_len[i] + 1 rows (at most q_stride) starting at position
@@ -759,7 +764,10 @@ def commit_metadata(start_pos: torch.Tensor, accept_len: torch.Tensor, q_stride:
     verify_metadata's outputs for those lengths, plus per commit row its
     verify row (int32, -1 past the committed rows) and its token (the verify
     argmax of that row, int64), and per sequence its last commit row
-    (int64)."""
+    (int64).  slot_offset shifts every row's slot and the sequence's key
+    count by that many positions: 1 is the reference's commit convention
+    (token i at slot start + 1 + i, context start + 2 + i,
+    model_runner.py:1143-1149), 0 this engine's (position p at slot p)."""
     lib = _native.load()
     _require_cuda(start_pos, accept_len, verify_argmax, block_tables, cu_seqlens_q, cu_seqlens_k,
                   positions, slot_mapping, verify_rows, token_ids, last_rows)
@@ -783,7 +791,7 @@ def commit_metadata(start_pos: torch.Tensor, accept_len: torch.Tensor, q_stride:
     check(lib.nva_commit_metadata(start_pos.data_ptr(), accept_len.data_ptr(), b, int(q_stride),
                                   verify_argmax.data_ptr(), verify_argmax.numel(),
                                   bt_ptr, bt_stride, bt_width, int(block_size),
-                                  cu_seqlens_q.data_ptr(),
+                                  int(slot_offset), cu_seqlens_q.data_ptr(),
                                   cu_seqlens_k.data_ptr(), positions.data_ptr(),
                                   slot_mapping.data_ptr(), verify_rows.data_ptr(),
                                   token_ids.data_ptr(), last_rows.data_ptr(), int(num_tokens),

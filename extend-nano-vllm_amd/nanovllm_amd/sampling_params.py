@@ -9,7 +9,12 @@ class SamplingParams:
     ignore_eos: bool = False
 
     def __post_init__(self):
-        if self.temperature < 0:
-            raise ValueError("temperature must be non-negative")
+        # the reference asserts (sampling_params.py:11); raised explicitly so
+        # the check survives python -O
+        if not self.temperature >= 0:
+            raise AssertionError("temperature must be non-negative")
+        # not in the reference: a budget of 0 tokens never reaches its
+        # stopping test (num_completion_tokens == max_tokens after a token is
+        # appended, scheduler.py:184-190) and would run to max_model_len
         if self.max_tokens < 1:
             raise ValueError("max_tokens must be at least 1")

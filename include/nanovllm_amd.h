@@ -379,14 +379,27 @@ int nva_verify_metadata(const int32_t *start_pos, const int32_t *q_lens, int32_t
  *   verify_argmax[0], position 0 and slot -1.
  * last_rows[i] = cu_seqlens_q[i+1] - 1 (int64).  num_seqs <= 2048; every
  *   array is device memory.
+ * Draft slot convention (slot_offset, 0 or 1; anything else is
+ *   NVA_ERR_ARG): the K/V of commit row t (RoPE position p = positions[t])
+ *   go to the slot of position p + slot_offset, and sequence i sees
+ *   cu_seqlens_k[i+1] - cu_seqlens_k[i] = start_pos[i] + q_i + slot_offset
+ *   keys, so row j of it sees the keys up to and including its own slot.
+ *   slot_offset = 1 is the reference's commit convention: token i of the
+ *   tail is written at slot start + 1 + i with context start + 2 + i
+ *   (nanovllm/engine/model_runner.py:1143-1149, _set_eagle3_commit_context
+ *   called from :1127-1156).  slot_offset = 0 writes position p at slot p,
+ *   as the reference's draft prefill does (:1379-1390) and this build's
+ *   engine does throughout.  A binder replacing the reference's commit loop
+ *   with this entry must use the same offset in nva_draft_metadata (or in
+ *   its own draft loop): the draft steps read the slots the commit wrote.
  * ------------------------------------------------------------------- */
 int nva_commit_metadata(const int32_t *start_pos, const int32_t *accept_len, int32_t num_seqs,
                         int32_t q_stride, const int32_t *verify_argmax, int32_t num_verify_rows,
                         const int32_t *block_tables, int64_t block_table_stride,
-                        int32_t max_blocks_per_seq, int32_t block_size, int32_t *cu_seqlens_q,
-                        int32_t *cu_seqlens_k, int64_t *positions, int32_t *slot_mapping,
-                        int32_t *verify_rows, int64_t *token_ids, int64_t *last_rows,
-                        int32_t num_tokens, void *stream);
+                        int32_t max_blocks_per_seq, int32_t block_size, int32_t slot_offset,
+                        int32_t *cu_seqlens_q, int32_t *cu_seqlens_k, int64_t *positions,
+                        int32_t *slot_mapping, int32_t *verify_rows, int64_t *token_ids,
+                        int64_t *last_rows, int32_t num_tokens, void *stream);
 
 /* Draft-step metadata for a draft queued right behind a verify, before the
  *   host has read its results.  Replaces the host loop that builds each
@@ -396,16 +409,26 @@ int nva_commit_metadata(const int32_t *start_pos, const int32_t *accept_len, int
  *   are padding) has length L_i = lens[i] + accept_len[verify_row[i]] + 1
  *   after the verified step (accept_len is the accept scan's output, indexed
  *   by the sequence's row in the verify batch), and its draft step s <
- *   steps is at position p = L_i - 1 + s: positions[s * bs + i] = p,
- *   context_lens[...] = p + 1, slot_mapping[...] = block id * block_size +
- *   p % block_size through block_tables row i (-1 where the block id is
- *   negative or p is past max_blocks_per_seq pages).  Padding columns get
- *   position 0, context 1 and slot -1.  Every array is device memory. */
+ *   steps is at RoPE position p = L_i - 1 + s: positions[s * bs + i] = p,
+ *   and with P = p + slot_offset, context_lens[...] = P + 1 and
+ *   slot_mapping[...] = block id * block_size + P % block_size through
+ *   block_tables row i (-1 where the block id is negative or P is past
+ *   max_blocks_per_seq pages).  Padding columns get position 0, context 1
+ *   and slot -1.  Every array is device memory.
+ * Draft slot convention (slot_offset, 0 or 1; anything else is
+ *   NVA_ERR_ARG): slot_offset = 1 is the reference's decode convention,
+ *   slot len(seq) + step and context len(seq) + step + 1 for the query at
+ *   RoPE position len(seq) - 1 + step (_set_eagle3_decode_context,
+ *   nanovllm/engine/model_runner.py:1087-1096).  slot_offset = 0 writes
+ *   position p at slot p with context p + 1, the convention of this
+ *   build's engine and of the reference's draft prefill (:1379-1390).  The
+ *   decode and commit loops of one engine must use the same offset
+ *   (nva_commit_metadata). */
 int nva_draft_metadata(const int64_t *lens, const int64_t *verify_row, const int32_t *accept_len,
                        int32_t num_seqs, int32_t bs, int32_t steps, const int32_t *block_tables,
                        int64_t block_table_stride, int32_t max_blocks_per_seq,
-                       int32_t block_size, int64_t *positions, int32_t *slot_mapping,
-                       int32_t *context_lens, void *stream);
+                       int32_t block_size, int32_t slot_offset, int64_t *positions,
+                       int32_t *slot_mapping, int32_t *context_lens, void *stream);
 
 /* Verify input ids composed on the device from the draft's proposals.
  *   Replaces the reference's verify input, each sequence's last

@@ -12,6 +12,9 @@ reference's host-side acceptance logic:
 * ``verify_greedy_proposals`` restates nanovllm/engine/speculative.py:11-30.
 * ``verify_metadata`` restates the per-token loops of prepare_prefill
   (nanovllm/engine/model_runner.py:761-800) for verify rows.
+* ``commit_metadata`` and ``draft_metadata`` restate the draft's commit
+  replay and draft-step contexts (model_runner.py:1087-1096, :1127-1156,
+  :1216-1249) in either draft slot convention (slot_offset 0 or 1).
 * ``reference_cpu_acceptance`` restates the per-sequence
   ``logits[start:end].argmax(dim=-1).tolist()`` loop of
   nanovllm/engine/model_runner.py:1066-1074 followed by
@@ -273,24 +276,33 @@ def reference_cpu_acceptance(logits, cu_q, input_ids):
     return accepted, bonus, committed
 
 
-def verify_metadata(start_pos, q_lens, block_tables, block_size, num_tokens):
+def _slot_of(row, position, block_size):
+    """Slot of a token position through one block-table row
+    (model_runner.py:784-789): -1 for a negative block id (the reference's
+    padding, :755-759) or a position past the row."""
+    idx = position // block_size
+    bid = int(row[idx]) if 0 <= idx < len(row) else -1
+    return bid * block_size + position % block_size if bid >= 0 else -1
+
+
+def verify_metadata(start_pos, q_lens, block_tables, block_size, num_tokens, slot_offset=0):
     """Restates prepare_prefill's per-sequence loop for verify rows
     (nanovllm/engine/model_runner.py:770-789): sequence i covers positions
     start .. start + q - 1, sees start + q keys, and token position p maps to
     slot block_table[p // block_size] * block_size + p % block_size.  Block
     ids of -1 (the reference's padding, :755-759) give slot -1 here, and rows
-    past the last sequence get position 0 and slot -1.  Returns int numpy
-    arrays (cu_q, cu_k, positions, slots)."""
+    past the last sequence get position 0 and slot -1.  slot_offset (draft
+    commits only) moves every row's K/V to the slot of position
+    p + slot_offset and the key count to start + q + slot_offset.  Returns
+    int numpy arrays (cu_q, cu_k, positions, slots)."""
     cu_q, cu_k, positions, slots = [0], [0], [], []
     for i, (start, q) in enumerate(zip(start_pos, q_lens)):
         cu_q.append(cu_q[-1] + int(q))
-        cu_k.append(cu_k[-1] + int(start) + int(q))
+        cu_k.append(cu_k[-1] + int(start) + int(q) + int(slot_offset))
         row = list(block_tables[i])
         for p in range(int(start), int(start) + int(q)):
             positions.append(p)
-            idx = p // block_size
-            bid = int(row[idx]) if idx < len(row) else -1
-            slots.append(bid * block_size + p % block_size if bid >= 0 else -1)
+            slots.append(_slot_of(row, p + int(slot_offset), block_size))
     pad = num_tokens - len(positions)
     positions += [0] * pad
     slots += [-1] * pad
@@ -299,7 +311,7 @@ def verify_metadata(start_pos, q_lens, block_tables, block_size, num_tokens):
 
 
 def commit_metadata(start_pos, accept_len, q_stride, verify_argmax, block_tables, block_size,
-                    num_tokens):
+                    num_tokens, slot_offset=0):
     """Restates what commit_eagle3 builds for one sequence
     (nanovllm/engine/model_runner.py:1216-1249: the output tokens, their
     positions start .. start + n - 1, the first n aux rows of the
@@ -308,11 +320,14 @@ def commit_metadata(start_pos, accept_len, q_stride, verify_argmax, block_tables
     tokens, the verify argmax of its rows i * q_stride .. + n_i - 1 (the
     accepted drafts equal the argmax of their rows; the last is the
     bonus).  Rows past the committed ones read verify row -1 -> token of
-    row 0.  Returns (cu_q, cu_k, positions, slots, verify_rows, token_ids,
-    last_rows) as numpy arrays."""
+    row 0.  slot_offset = 1 is the reference's slots and contexts
+    (_commit_eagle3_tokens, :1127-1156: token i at slot start + 1 + i,
+    context start + 2 + i); 0 stores position p at slot p.  Returns
+    (cu_q, cu_k, positions, slots, verify_rows, token_ids, last_rows) as
+    numpy arrays."""
     n = [min(max(int(a), 0) + 1, int(q_stride)) for a in accept_len]
     cu_q, cu_k, positions, slots = verify_metadata(start_pos, n, block_tables, block_size,
-                                                   num_tokens)
+                                                   num_tokens, slot_offset)
     rows = []
     for i, ni in enumerate(n):
         rows += [i * int(q_stride) + j for j in range(ni)]
@@ -322,3 +337,29 @@ def commit_metadata(start_pos, accept_len, q_stride, verify_argmax, block_tables
     last = [int(cu_q[i + 1]) - 1 for i in range(len(n))]
     return (cu_q, cu_k, positions, slots, np.array(rows, np.int32), np.array(ids, np.int64),
             np.array(last, np.int64))
+
+
+def draft_metadata(lens, verify_row, accept_len, num_seqs, bs, steps, block_tables, block_size,
+                   slot_offset=0):
+    """Restates the per-step loop of propose_eagle3_batch /
+    _set_eagle3_decode_context (nanovllm/engine/model_runner.py:1087-1096,
+    :1190-1203) for the draft queued behind a verify: column i < num_seqs
+    is a sequence of length L = lens[i] + accept_len[verify_row[i]] + 1
+    after the verified step; its step s queries RoPE position
+    p = L - 1 + s, writes its K/V at the slot of position p + slot_offset and
+    sees p + slot_offset + 1 keys (the reference: slot len + step, context
+    len + step + 1, i.e. slot_offset = 1).  Padding columns get position 0,
+    slot -1 and context 1.  Returns int numpy arrays [steps, bs]
+    (positions int64, slots int32, contexts int32)."""
+    pos = np.zeros((steps, bs), np.int64)
+    slots = np.full((steps, bs), -1, np.int32)
+    ctx = np.ones((steps, bs), np.int32)
+    for i in range(num_seqs):
+        length = int(lens[i]) + int(accept_len[int(verify_row[i])]) + 1
+        row = list(block_tables[i])
+        for step in range(steps):
+            p = length - 1 + step
+            pos[step, i] = p
+            slots[step, i] = _slot_of(row, p + int(slot_offset), block_size)
+            ctx[step, i] = p + int(slot_offset) + 1
+    return pos, slots, ctx

@@ -106,13 +106,21 @@ def test_host_side_argument_errors_without_gpu():
         _native.check(_native.NVA_ERR_CAPACITY, "probe")
     # commit metadata: a zero verify stride, a missing accept buffer and more
     # sequences than the one-workgroup scan holds are refused on the host
-    assert lib.nva_commit_metadata(fake, fake, 2, 0, fake, 12, fake, 4, 4, 256, fake, fake, fake,
-                                   fake, fake, fake, fake, 12, None) == _native.NVA_ERR_ARG
-    assert lib.nva_commit_metadata(fake, None, 2, 6, fake, 12, fake, 4, 4, 256, fake, fake, fake,
-                                   fake, fake, fake, fake, 12, None) == _native.NVA_ERR_ARG
-    assert lib.nva_commit_metadata(fake, fake, 2049, 6, fake, 12, fake, 4, 4, 256, fake, fake,
+    assert lib.nva_commit_metadata(fake, fake, 2, 0, fake, 12, fake, 4, 4, 256, 0, fake, fake,
+                                   fake, fake, fake, fake, fake, 12, None) == _native.NVA_ERR_ARG
+    assert lib.nva_commit_metadata(fake, None, 2, 6, fake, 12, fake, 4, 4, 256, 0, fake, fake,
+                                   fake, fake, fake, fake, fake, 12, None) == _native.NVA_ERR_ARG
+    assert lib.nva_commit_metadata(fake, fake, 2049, 6, fake, 12, fake, 4, 4, 256, 0, fake, fake,
                                    fake, fake, fake, fake, fake, 12,
                                    None) == _native.NVA_ERR_UNSUPPORTED
+    # the draft slot convention is 0 (slot p) or 1 (the reference's slot
+    # p + 1); any other offset is refused by both draft-side entries
+    for off in (-1, 2):
+        assert lib.nva_commit_metadata(fake, fake, 2, 6, fake, 12, fake, 4, 4, 256, off, fake,
+                                       fake, fake, fake, fake, fake, fake, 12,
+                                       None) == _native.NVA_ERR_ARG
+        assert lib.nva_draft_metadata(fake, fake, fake, 2, 4, 3, fake, 4, 4, 256, off, fake,
+                                      fake, fake, None) == _native.NVA_ERR_ARG
     # zero-size work is a no-op
     assert lib.nva_argmax_rows(None, 8, 8, 0, None, None, None, 0, None) == _native.NVA_OK
     assert lib.nva_argmax_workspace_size(384, 64, 151936) > 0

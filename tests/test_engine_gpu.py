@@ -444,3 +444,82 @@ def test_prelaunched_drafts_equal_fresh_drafts(dirs):
     assert len(raw_on) == len(raw_off)
     for step, (a, b) in enumerate(zip(raw_on, raw_off)):
         assert torch.equal(a, b), step
+
+
+def test_prelaunched_drafts_with_the_device_running_behind(dirs, monkeypatch):
+    """The queued device commit and next-step draft take their metadata from
+    pinned staging buffers the host refills every step.  Here the draft
+    override rewrites the proposals with device work only (no host sync),
+    and a spin kernel is queued ahead of every device commit, so the host
+    reaches the next step's refill while the previous step's copies are
+    still queued.  The raw draft tokens of every step must equal those of
+    an engine that drafts after the host's bookkeeping, and the refills
+    must have found copies still queued (the case the staging's wait
+    covers)."""
+    from nanovllm_amd.engine import graphs
+
+    ps = [prompts(1, seed=41, lo=250, hi=258)[0], prompts(1, seed=42, lo=20, hi=30)[0],
+          prompts(1, seed=43, lo=500, hi=510)[0]]
+    max_tokens = [60, 54, 48]
+    plain = make_llm(dirs, spec=False)
+    try:
+        ref = [plain.generate([p], SamplingParams(temperature=0.0, max_tokens=m, ignore_eos=True),
+                              use_tqdm=False)[0]["token_ids"] for p, m in zip(ps, max_tokens)]
+    finally:
+        plain.exit()
+    full = {tuple(p): p + r for p, r in zip(ps, ref)}
+
+    orig_run = graphs.DeviceCommitGraph.run
+
+    def run_behind(self, state_rows):
+        torch.cuda._sleep(3_000_000)        # a few ms of spinning ahead of the copy
+        orig_run(self, state_rows)
+
+    def run(prelaunch, slow):
+        raw, calls = [], {"n": 0}
+
+        def override(seqs, tokens):
+            k, bs = tokens.shape
+            raw.append(tokens[:, :len(seqs)].clone())          # stays on the device
+            want = torch.zeros(k, bs, dtype=torch.int64, pin_memory=True)
+            for i, seq in enumerate(seqs):
+                cont = full[tuple(seq.prompt_token_ids)][len(seq):len(seq) + k]
+                calls["n"] += 1
+                for s_, tok in enumerate(cont):
+                    want[s_, i] = tok
+                if calls["n"] % 4 == 0:
+                    want[calls["n"] % k, i] = (int(want[calls["n"] % k, i]) + 1) % 2048
+            tokens.copy_(want.to(tokens.device, non_blocking=True))
+
+        if slow:
+            monkeypatch.setattr(graphs.DeviceCommitGraph, "run", run_behind)
+        else:
+            monkeypatch.setattr(graphs.DeviceCommitGraph, "run", orig_run)
+        llm = make_llm(dirs, spec=True, k=5, eager=False)
+        llm.prelaunch_draft = prelaunch
+        llm.model_runner.draft_override = override
+        try:
+            for p, m in zip(ps, max_tokens):
+                llm.add_request(p, SamplingParams(temperature=0.0, max_tokens=m, ignore_eos=True))
+            outs = {}
+            while not llm.is_finished():
+                for seq_id, toks in llm.step()[0]:
+                    outs[seq_id] = toks
+            runner = llm.model_runner
+            waits = sum(g.i64.waits for g in runner._device_commit_graphs.values())
+            waits += sum(g.meta.waits + g.meta32.waits for g in runner._chained_graphs.values())
+            return ([outs[i] for i in sorted(outs)], [r.cpu() for r in raw],
+                    dict(llm.spec_stats), dict(runner.prelaunch_stats), waits)
+        finally:
+            llm.exit()
+
+    got_on, raw_on, stats_on, pre_on, waits_on = run(True, slow=True)
+    got_off, raw_off, stats_off, pre_off, _ = run(False, slow=False)
+    print(f"prelaunch {pre_on}, refills that waited for a queued copy: {waits_on}", flush=True)
+    assert pre_on["used"] >= 5, pre_on
+    assert waits_on > 0
+    assert stats_on == stats_off and stats_on["accepted"] > stats_on["steps"]
+    assert got_on == got_off
+    assert len(raw_on) == len(raw_off)
+    for step, (a, b) in enumerate(zip(raw_on, raw_off)):
+        assert torch.equal(a, b), step

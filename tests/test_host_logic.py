@@ -509,3 +509,16 @@ def test_draft_steps_past_a_sequence_limit_write_nowhere(cpu_runner):
     assert [row[0] for row in slots] == [-1, -1, -1, -1]
     assert [row[1] for row in slots] == [far.block_table[0] * BS + p for p in (40, 41, 42, 43)]
     assert [row[1] for row in ctx] == [41, 42, 43, 44]
+
+
+def test_sampling_params_errors_follow_the_reference():
+    """A negative temperature fails the reference's assert
+    (sampling_params.py:11), so it raises AssertionError here too; a zero
+    token budget (which the reference does not check) is refused up front."""
+    with pytest.raises(AssertionError, match="temperature must be non-negative"):
+        SamplingParams(temperature=-0.5)
+    with pytest.raises(AssertionError):
+        SamplingParams(temperature=float("nan"))
+    with pytest.raises(ValueError, match="max_tokens"):
+        SamplingParams(max_tokens=0)
+    assert SamplingParams(temperature=0.0, max_tokens=1).max_tokens == 1

@@ -549,13 +549,15 @@ def test_verify_metadata_matches_oracle(K, cuda, num_seqs, seed):
     np.testing.assert_array_equal(o_slots.cpu().numpy(), slots)
 
 
+@pytest.mark.parametrize("slot_offset", [0, 1])
 @pytest.mark.parametrize("num_seqs,q_stride,seed",
                          [(1, 6, 0), (64, 6, 1), (300, 8, 2), (5, 1, 3), (0, 6, 4)])
-def test_commit_metadata_matches_oracle(K, cuda, num_seqs, q_stride, seed):
+def test_commit_metadata_matches_oracle(K, cuda, num_seqs, q_stride, seed, slot_offset):
     """Device metadata of the draft's replay of the committed tails:
     bit-exact against the restatement, from accept lengths taken straight
     from an accept-scan-shaped buffer (including out-of-range ones, which
-    clamp), with -1 block ids, page crossings and padding rows."""
+    clamp), with -1 block ids, page crossings and padding rows, in both
+    draft slot conventions (0: slot p; 1: the reference's slot p + 1)."""
     g = np.random.default_rng(seed)
     bs, width = 256, 12
     accept = g.integers(0, q_stride, num_seqs).astype(np.int32)
@@ -566,7 +568,7 @@ def test_commit_metadata_matches_oracle(K, cuda, num_seqs, q_stride, seed):
     tables[g.random((num_seqs, width)) < 0.05] = -1
     t = max(num_seqs * q_stride, 5)
     argmax = g.integers(0, 151936, t).astype(np.int32)
-    ref = oracle.commit_metadata(start, accept, q_stride, argmax, tables, bs, t)
+    ref = oracle.commit_metadata(start, accept, q_stride, argmax, tables, bs, t, slot_offset)
     d = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(cuda)
     # the engine passes slices of the accept scan's one int32 buffer
     out = d(np.concatenate([argmax, accept, np.full(num_seqs, -9, np.int32)]))
@@ -578,7 +580,8 @@ def test_commit_metadata_matches_oracle(K, cuda, num_seqs, q_stride, seed):
     o_ids = torch.full((t,), -7, dtype=torch.int64, device=cuda)
     o_last = torch.full((num_seqs,), -7, dtype=torch.int64, device=cuda)
     K.commit_metadata(d(start), out[t:t + num_seqs], q_stride, out[:t], d(tables), bs, t,
-                      o_cu_q, o_cu_k, o_pos, o_slots, o_rows, o_ids, o_last)
+                      o_cu_q, o_cu_k, o_pos, o_slots, o_rows, o_ids, o_last,
+                      slot_offset=slot_offset)
     torch.cuda.synchronize()
     for got, want in zip((o_cu_q, o_cu_k, o_pos, o_slots, o_rows, o_ids, o_last), ref):
         np.testing.assert_array_equal(got.cpu().numpy(), want)
@@ -1061,3 +1064,14 @@ def test_draft_metadata_after_verify(K, cuda):
     assert torch.equal(slots.cpu(), want_slot)
     assert torch.equal(ctx.cpu(), (want_pos + 1).to(torch.int32))
     assert (want_slot[:, 3] == -1).any() and (want_slot[:, b:] == -1).all()
+    # both draft slot conventions against the oracle's restatement (offset 1
+    # is the reference's slot len + step, context len + step + 1)
+    for off in (0, 1):
+        K.draft_metadata(lens.to(cuda), vrow.to(cuda), accept.to(cuda), b, bt.to(cuda), bsz, pos,
+                         slots, ctx, slot_offset=off)
+        torch.cuda.synchronize()
+        opos, oslots, octx = oracle.draft_metadata(lens.numpy(), vrow.numpy(), accept.numpy(), b,
+                                                   bs, steps, bt.numpy(), bsz, off)
+        np.testing.assert_array_equal(pos.cpu().numpy(), opos)
+        np.testing.assert_array_equal(slots.cpu().numpy(), oslots)
+        np.testing.assert_array_equal(ctx.cpu().numpy(), octx)

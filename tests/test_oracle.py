@@ -378,6 +378,104 @@ def test_commit_metadata_hand_worked():
     assert last.tolist() == [0, 3]
 
 
+def test_commit_metadata_reference_slot_convention_hand_worked():
+    """The reference's commit (_commit_eagle3_tokens, model_runner.py:
+    1127-1156) writes tail token i of a commit starting at start_position s
+    at slot position s + 1 + i with context s + 2 + i.  Worked by hand for
+    s = 254, three tokens, block table [7, 2] (256-token pages): slot
+    positions 255, 256, 257 -> slots 7*256+255, 2*256+0, 2*256+1, contexts
+    256, 257, 258.  The batched form gives the sequence 258 keys, so its
+    bottom-right aligned row j sees 258 - 3 + j + 1 = 256 + j keys, the
+    reference's context for token j.  With slot_offset 0 every position
+    keeps its own slot (254 -> 7*256+254) and the sequence 257 keys."""
+    am = list(range(100, 106))
+    cu_q, cu_k, pos, slots, rows, ids, last = oracle.commit_metadata(
+        [254], [2], 6, am, [[7, 2]], 256, 4, slot_offset=1)
+    assert pos.tolist() == [254, 255, 256, 0]
+    assert slots.tolist() == [7 * 256 + 255, 2 * 256 + 0, 2 * 256 + 1, -1]
+    assert cu_q.tolist() == [0, 3] and cu_k.tolist() == [0, 258]
+    n_keys = int(cu_k[1] - cu_k[0])
+    assert [n_keys - 3 + j + 1 for j in range(3)] == [256, 257, 258]
+    assert rows.tolist() == [0, 1, 2, -1] and ids.tolist() == [100, 101, 102, 100]
+    assert last.tolist() == [2]
+    cu_q, cu_k, pos, slots, *_ = oracle.commit_metadata([254], [2], 6, am, [[7, 2]], 256, 4)
+    assert pos.tolist() == [254, 255, 256, 0]
+    assert slots.tolist() == [7 * 256 + 254, 7 * 256 + 255, 2 * 256 + 0, -1]
+    assert cu_k.tolist() == [0, 257]
+    # the reference's slot for the last committed token may fall in a page
+    # the table does not have: slot -1 (no write) rather than an error
+    _, _, _, slots, *_ = oracle.commit_metadata([510], [1], 6, am, [[7, 2]], 256, 2,
+                                                slot_offset=1)
+    assert slots.tolist() == [2 * 256 + 255, -1]
+
+
+def test_draft_metadata_reference_slot_convention_hand_worked():
+    """_set_eagle3_decode_context (model_runner.py:1087-1096): for a
+    sequence of len(seq) tokens, draft step `step` queries RoPE position
+    len - 1 + step, writes slot position len + step and sees len + step + 1
+    keys.  Worked by hand: length 253 before the verify, one accepted draft
+    plus the bonus -> len 255 after it; block table [7, 2, -1]; three
+    steps.  Reference (offset 1): slot positions 255, 256, 257 -> slots
+    2047, 512, 513, contexts 256, 257, 258.  Offset 0: slot positions 254,
+    255, 256 -> 2046, 2047, 512, contexts 255, 256, 257.  The second column
+    is padding (position 0, slot -1, context 1); a third sequence's late
+    steps run past its one-page table (slot -1)."""
+    lens, vrow, accept = [253, 0, 250], [1, 0, 2], [9, 1, 3]
+    tables = [[7, 2, -1], [-1, -1, -1], [4, -1, -1]]
+    pos, slots, ctx = oracle.draft_metadata(lens, vrow, accept, 1, 2, 3, tables, 256,
+                                            slot_offset=1)
+    assert pos.tolist() == [[254, 0], [255, 0], [256, 0]]
+    assert slots.tolist() == [[2047, -1], [512, -1], [513, -1]]
+    assert ctx.tolist() == [[256, 1], [257, 1], [258, 1]]
+    pos, slots, ctx = oracle.draft_metadata(lens, vrow, accept, 1, 2, 3, tables, 256)
+    assert pos.tolist() == [[254, 0], [255, 0], [256, 0]]
+    assert slots.tolist() == [[2046, -1], [2047, -1], [512, -1]]
+    assert ctx.tolist() == [[255, 1], [256, 1], [257, 1]]
+    # the third sequence: 250 + 3 + 1 = 254 tokens; reference slot
+    # positions 254, 255, 256 -> 4*256+254, 4*256+255, past the table
+    pos, slots, ctx = oracle.draft_metadata([lens[2]], [0], [3], 1, 1, 3, [tables[2]], 256,
+                                            slot_offset=1)
+    assert pos[:, 0].tolist() == [253, 254, 255]
+    assert slots[:, 0].tolist() == [4 * 256 + 254, 4 * 256 + 255, -1]
+    assert ctx[:, 0].tolist() == [255, 256, 257]
+
+
+def test_draft_metadata_offset_zero_agrees_with_engine_host_loop():
+    """Offset 0 is what the engine's own host loop builds for a fresh draft
+    (ModelRunner._draft_step_metadata, written independently): the same
+    positions, slots and contexts for sequences of the post-verify
+    lengths, on random batches."""
+    import random
+
+    from nanovllm_amd.engine import model_runner as mr
+    from nanovllm_amd.engine.sequence import Sequence
+
+    rng = random.Random(17)
+    runner = mr.ModelRunner.__new__(mr.ModelRunner)
+    runner.block_size = 256
+    for trial in range(10):
+        b, k = rng.randrange(1, 9), rng.randrange(2, 8)
+        lens = [rng.randrange(1, 1200) for _ in range(b)]
+        accept = [rng.randrange(0, k) for _ in range(b)]
+        vrow = list(range(b))
+        rng.shuffle(vrow)
+        acc_by_row = [0] * b
+        for i in range(b):
+            acc_by_row[vrow[i]] = accept[i]
+        seqs, tables = [], []
+        for n, a in zip(lens, accept):
+            seq = Sequence(list(range(n + a + 1)))
+            seq.block_table = rng.sample(range(5000), -(-(n + a + k + 1) // 256))
+            seqs.append(seq)
+            tables.append(seq.block_table)
+        pos, slots, ctx = runner._draft_step_metadata(seqs, [k] * b, k)
+        opos, oslots, octx = oracle.draft_metadata(lens, vrow, acc_by_row, b, b, k - 1, tables,
+                                                   256)
+        assert opos.tolist() == pos.tolist(), trial
+        assert oslots.tolist() == slots.tolist(), trial
+        assert octx.tolist() == ctx.tolist(), trial
+
+
 def test_commit_metadata_agrees_with_torch_gather_formulation():
     """The rows, tokens and last rows as a torch searchsorted / where /
     index_select chain over the verify batch (an independent formulation)
