@@ -53,7 +53,36 @@ DEFAULT_GEMM_TUNING = os.path.join(ROOT, "extend-nano-vllm_amd", "nanovllm_amd",
 # whose shapes it was measured on.
 PMC_TRAFFIC_BYTES = int((158671.6 * 2.0 + 3072.0 * 1.0) * 1024)
 PMC_WORKLOAD = dict(preset="qwen3-8b", batch=64, k=5, prompt_min=256, prompt_max=2048,
-                    max_tokens=256, seed=2)
+                    max_tokens=256, seed=2, kv_layout="head_major")
+# the kernel source the counters were read on (sha256 of csrc/paged_attention.hip
+# then csrc/common.h, first 16 hex digits): the constant is quoted only while
+# the source is unchanged, since a change of the kernel's loads changes it
+PMC_ATTENTION_SOURCE = "0000000000000000"
+ATTENTION_SOURCES = ("paged_attention.hip", "common.h")
+
+
+def attention_source_hash() -> str:
+    import hashlib
+
+    h = hashlib.sha256()
+    for name in ATTENTION_SOURCES:
+        with open(os.path.join(ROOT, "extend-nano-vllm_amd", "csrc", name), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
+def pmc_traffic_reason(args) -> str | None:
+    """Why the recorded traffic constant does not apply (None when it does)."""
+    if not all(getattr(args, key) == val for key, val in PMC_WORKLOAD.items()):
+        return "the counters were read on the default workload only"
+    if attention_source_hash() != PMC_ATTENTION_SOURCE:
+        return (f"the attention kernel's source ({attention_source_hash()}) is not the one the "
+                f"counters were read on ({PMC_ATTENTION_SOURCE})")
+    return None
+
+
+def pmc_traffic_bytes(args) -> int | None:
+    return PMC_TRAFFIC_BYTES if pmc_traffic_reason(args) is None else None
 METRIC = "accepted tok/s, Qwen3-8B EAGLE3 k=5 bs64; verify-attn HBM GB/s % of peak"
 
 
@@ -798,9 +827,10 @@ def make_engine(args, tmp: str):
                                    "aux_hidden_state_layers": aux})
 
 
-def add_prompts(llm, args):
+def add_prompts(llm, args, seq_row: dict | None = None):
     """The seeded prompts (lengths U[prompt_min, prompt_max], random ids);
-    returns the prompt token lists in request order."""
+    returns the prompt token lists in request order.  seq_row (optional)
+    receives each new sequence's id -> its row in that order."""
     import torch
 
     from nanovllm_amd import SamplingParams
@@ -813,6 +843,8 @@ def add_prompts(llm, args):
     for L in lens:
         prompts.append(torch.randint(0, vocab, (L,), generator=g).tolist())
         llm.add_request(prompts[-1], sp)
+        if seq_row is not None:
+            seq_row[llm.scheduler.waiting[-1].seq_id] = len(prompts) - 1
     return prompts
 
 
@@ -866,6 +898,71 @@ def timed_steps(llm, steps: int):
     return elapsed, committed, stats
 
 
+def generation(llm, warmup: int, steps: int, seq_row: dict):
+    """Every decode step of the batch, from the first one after prefill to the
+    last sequence's finish (the reference's decode throughput covers the
+    whole generate(), llm_engine.py:175-185, :200-219), with the bench
+    line's window inside it: after ``warmup`` steps, ``steps`` steps
+    bracketed by synchronisations (the window's two synchronisations are
+    the only ones the generation adds).  Returns (whole, window, outputs):
+    whole / window = dicts of seconds, engine steps, committed tokens,
+    speculation counters, mean keys per sequence at the start and end;
+    outputs = {request row: completion token ids}."""
+    import torch
+
+    def mean_keys():
+        run = llm.scheduler.running
+        return round(sum(len(x) for x in run) / max(len(run), 1), 1)
+
+    before = dict(llm.spec_stats)
+    pre_before = dict(llm.model_runner.prelaunch_stats)
+    outputs, n, committed = {}, 0, 0
+    window = None
+    keys0 = mean_keys()
+    torch.cuda.synchronize()
+    t_start = time.perf_counter()
+    while not llm.is_finished():
+        if n == warmup:
+            torch.cuda.synchronize()
+            w0, w_committed, w_keys = time.perf_counter(), committed, mean_keys()
+            w_stats = dict(llm.spec_stats)
+            w_pre = dict(llm.model_runner.prelaunch_stats)
+        out, num_tokens = llm.step()
+        if num_tokens > 0:
+            raise RuntimeError("a prefill step inside the decode generation")
+        committed += -num_tokens
+        n += 1
+        for seq_id, toks in out:
+            outputs[seq_row[seq_id]] = toks
+        if n == warmup + steps:
+            torch.cuda.synchronize()
+            w1 = time.perf_counter()
+            window = {"seconds": w1 - w0, "steps": steps, "committed": committed - w_committed,
+                      "keys_start": w_keys, "keys_end": mean_keys(),
+                      "stats": {k: llm.spec_stats[k] - w_stats[k] for k in w_stats},
+                      "prelaunch": {k: llm.model_runner.prelaunch_stats[k] - w_pre[k]
+                                    for k in w_pre}}
+    torch.cuda.synchronize()
+    seconds = time.perf_counter() - t_start
+    whole = {"seconds": seconds, "steps": n, "committed": committed, "keys_start": keys0,
+             "stats": {k: llm.spec_stats[k] - before[k] for k in before},
+             "prelaunch": {k: llm.model_runner.prelaunch_stats[k] - pre_before[k]
+                           for k in pre_before}}
+    return whole, window, outputs
+
+
+def generation_record(whole: dict, n_seqs: int, note: str) -> dict:
+    st = whole["stats"]
+    seq_steps = max(st["steps"], 1) * n_seqs
+    return {"value": round(whole["committed"] / whole["seconds"], 1), "unit": "tok/s",
+            "seconds": round(whole["seconds"], 3), "steps": whole["steps"],
+            "ms_per_step": round(whole["seconds"] / max(whole["steps"], 1) * 1e3, 3),
+            "committed_tokens": whole["committed"], "sequences": n_seqs,
+            "mean_keys_per_seq_at_start": whole["keys_start"],
+            "accepted_drafts": st["accepted"], "drafted": st["drafted"],
+            "prelaunched_drafts": whole["prelaunch"], "note": note}
+
+
 def reference_steps(llm, steps: int, torch_attention: bool):
     """The reference's step structure (llm_engine.py:124-178): one warm-up
     step, then ``steps`` timed ones; on this build's attention kernel or on
@@ -901,7 +998,9 @@ def forced_acceptance(args, tmp: str, continuations):
     the main run, each draft position keeping the target's token with
     probability args.draft_keep (a seeded choice per sequence and position)
     and otherwise a different id.  The rewrite is one small host-to-device
-    copy and one gather per step inside the timed region."""
+    copy and one gather per step inside the timed region.  Timed like the
+    main run: the whole generation, with a window of 3 + args.acceptance_steps
+    steps at its start."""
     import torch
 
     llm = make_engine(args, tmp)
@@ -927,25 +1026,37 @@ def forced_acceptance(args, tmp: str, continuations):
         pos = info[b:][None, :] + torch.arange(k, device=tokens.device)[:, None]
         tokens[:, :b] = table[info[:b][None, :].expand(k, b), pos]
 
+    seq_row = dict(row_of)
     try:
         while llm.scheduler.waiting:
             llm.step()
         runner.draft_override = override
-        for _ in range(3):
-            llm.step()
         n_active = len(llm.scheduler.running)
-        elapsed, committed, stats = timed_steps(llm, args.acceptance_steps)
+        whole, window, outputs = generation(llm, 3, args.acceptance_steps, seq_row)
     finally:
         runner.draft_override = None
         release(llm)
+    if window is None:
+        raise RuntimeError("the forced-acceptance generation ended inside its timed window")
+    stats = window["stats"]
     seq_steps = max(stats["steps"] * n_active, 1)
-    return {"value": round(committed / elapsed, 1), "unit": "tok/s",
-            "ms_per_step": round(elapsed / args.acceptance_steps * 1e3, 3),
+    # the forced drafts only reorder how the target's tokens are committed:
+    # every sequence must end with the main run's greedy continuation
+    same = sum(outputs[i] == continuations[tuple(p)][len(p):] for i, p in enumerate(prompts))
+    wst = whole["stats"]
+    return {"value": round(window["committed"] / window["seconds"], 1), "unit": "tok/s",
+            "ms_per_step": round(window["seconds"] / args.acceptance_steps * 1e3, 3),
             "steps": args.acceptance_steps, "warmup": 3, "active_seqs": n_active,
             "draft_keep": args.draft_keep,
             "accepted_drafts_per_seq_step": round(stats["accepted"] / seq_steps, 4),
             "mean_acceptance_length": round(stats["committed"] / seq_steps, 4),
             "position_accept_rate": round(stats["accepted"] / max(stats["drafted"], 1), 4),
+            "whole_generation": dict(generation_record(
+                whole, n_active, "every decode step from the first after prefill to the last "
+                "finished sequence, forced drafts (the window above is its steps 4-23)"),
+                mean_acceptance_length=round(wst["committed"] / max(wst["steps"] * n_active, 1),
+                                             4)),
+            "outputs_equal_main_run": f"{same} of {len(prompts)}",
             "drafts": "target-greedy continuation of each sequence (recorded by the main run, "
                       "whose steps commit exactly the target's argmax), kept per position with "
                       "probability draft_keep"}
@@ -1129,21 +1240,41 @@ def main():
     llm = make_engine(args, tmp)
     runner = llm.model_runner
     log(f"engine up: {runner.get_diagnostics()}")
-    prompts = add_prompts(llm, args)
+    seq_row = {}
+    prompts = add_prompts(llm, args, seq_row)
 
     t_setup = time.perf_counter()
     while llm.scheduler.waiting:
         llm.step()
-    log(f"prefill done in {time.perf_counter() - t_setup:.1f}s")
-    for _ in range(args.warmup):
-        llm.step()
-    log("warmup done")
     torch.cuda.synchronize()
     setup_s = time.perf_counter() - t_setup
+    log(f"prefill done in {setup_s:.1f}s")
+    n_active = len(llm.scheduler.running)
 
-    # capture verify batches for the CPU baseline (outside the timed region)
-    cpu_batches = []
-    runner.keep_verify_inputs = True
+    # the whole generation, first decode step to last finished sequence, with
+    # the line's window (W warm-up steps, then the K timed steps) at its start
+    whole, window, outputs = generation(llm, args.warmup, args.steps, seq_row)
+    if window is None:
+        raise RuntimeError(f"the generation ended within {args.warmup} + {args.steps} steps")
+    elapsed, committed, stats = window["seconds"], window["committed"], window["stats"]
+    stats["prelaunch"] = window["prelaunch"]
+    log(f"timed {args.steps} steps in {elapsed:.3f}s; whole generation: {whole['steps']} steps "
+        f"in {whole['seconds']:.3f}s")
+    # zero acceptance (random draft): every committed token is the target's
+    # argmax, so the outputs are the target-greedy continuations the
+    # forced-acceptance run replays as drafts
+    continuations = {tuple(p): p + outputs[i] for i, p in enumerate(prompts)}
+
+    # the same prompts again, for the measurements that need live sequences
+    # and perturb a step (eager verify launches, host syncs): the CPU
+    # baseline's logits, the roofline's attention launches, the
+    # reference-structured steps
+    add_prompts(llm, args, {})
+    while llm.scheduler.waiting:
+        llm.step()
+    for _ in range(args.warmup):
+        llm.step()
+    profiled_steps(llm, args.profile_steps)
 
     orig_verify = runner.verify_eagle3_batch_fused
 
@@ -1155,17 +1286,14 @@ def main():
             timer.current_lens = None
 
     runner.verify_eagle3_batch_fused = verify_with_lens
+    cpu_batches = []
     if not args.no_cpu_baseline:
+        runner.keep_verify_inputs = True
         llm.step()
         logits, cu, ids = runner.last_verify_inputs
         cpu_batches.append((logits.cpu(), list(cu), ids.cpu().tolist()))
-    runner.keep_verify_inputs = False
-    runner.last_verify_inputs = None
-
-    n_active = len(llm.scheduler.running)
-    elapsed, committed, stats = timed_steps(llm, args.steps)
-    log(f"timed {args.steps} steps in {elapsed:.3f}s")
-    profiled_steps(llm, args.profile_steps)
+        runner.keep_verify_inputs = False
+        runner.last_verify_inputs = None
 
     # roofline: one more step of the same workload with the verify forward
     # launched eagerly (events cannot be recorded inside a captured HIP graph
@@ -1176,29 +1304,16 @@ def main():
     llm.step()
     timer.capture = False
     runner.use_verify_graph = True
-    default_workload = all(getattr(args, key) == val for key, val in PMC_WORKLOAD.items())
-    roof = timer.measure(args.roofline_repeats, PMC_TRAFFIC_BYTES if default_workload else None)
+    traffic = pmc_traffic_bytes(args)
+    roof = timer.measure(args.roofline_repeats, traffic)
     if roof is not None:
         roof["traffic_source"] = (
             "recorded constant (not measured by this run): rocprofv3 --pmc FETCH_SIZE then "
             "WRITE_SIZE over `bench.py --attention-only` on this workload, scaled by the same "
-            "counters' readings for a 1 GiB device copy and a 1 GiB read; "
-            "profiles/verify_attention_traffic_qwen3_8b_bs64.md" if default_workload else
-            "not measured for this workload")
-
-    # the target's greedy continuation of every sequence for the
-    # forced-acceptance run: the graphed steps commit exactly the target's
-    # argmax (the random draft is never accepted), so stepping on records it
-    continuations = None
-    if args.acceptance_steps > 0:
-        need = (3 + args.acceptance_steps + 2) * (args.k + 1)
-        while llm.scheduler.running and min(
-                s.num_completion_tokens for s in llm.scheduler.running) < need:
-            llm.step()
-        continuations = {tuple(s.prompt_token_ids): list(s.token_ids)
-                         for s in llm.scheduler.running}
-        if len(continuations) != len(prompts):
-            continuations = None   # a sequence finished (max_tokens too small)
+            "counters' readings for a 1 GiB device copy and a 1 GiB read, measured on "
+            f"paged_attention.hip sha256[:16] {PMC_ATTENTION_SOURCE}; "
+            "profiles/verify_attention_traffic_qwen3_8b_bs64.md" if traffic is not None else
+            "null: " + pmc_traffic_reason(args))
 
     ref = ref_torch = None
     if args.reference_steps > 0 and llm.scheduler.running:
@@ -1212,10 +1327,11 @@ def main():
     release(llm)
 
     forced = None
-    if continuations is not None:
+    if args.acceptance_steps > 0:
         forced = forced_acceptance(args, tmp, continuations)
         log(f"forced acceptance: {forced['value']} tok/s, {forced['ms_per_step']} ms/step, "
-            f"mean acceptance length {forced['mean_acceptance_length']}")
+            f"mean acceptance length {forced['mean_acceptance_length']}; whole generation "
+            f"{forced['whole_generation']['value']} tok/s")
     per_config_after = None
     if not args.no_per_config:
         per_config_after = [{k: v for k, v in rec.items() if k != "cpu_baseline"}
@@ -1244,6 +1360,13 @@ def main():
         "roofline": roof,
         "cpu_baseline": cpu,
         "committed_tokens": committed,
+        "window": {"position": f"decode steps {args.warmup + 1}-{args.warmup + args.steps} of "
+                               f"{whole['steps']}",
+                   "mean_keys_per_seq": [window["keys_start"], window["keys_end"]]},
+        "whole_generation": generation_record(
+            whole, n_active, "every decode step from the first after prefill to the last "
+            "finished sequence, in the run that holds the timed window (its only extra "
+            "synchronisations are the window's two)"),
         "accepted_drafts_per_seq_step": round(stats["accepted"] / max(stats["steps"] * n_active, 1), 4),
         "committed_per_seq_step": round(stats["committed"] / max(stats["steps"] * n_active, 1), 4),
         "prelaunched_drafts": dict(stats["prelaunch"], note=(

@@ -27,9 +27,9 @@ from nanovllm_amd import _native
 from nanovllm_amd import kernels as K
 from nanovllm_amd.context import get_context, reset_context, set_context
 from nanovllm_amd.eagle3 import Eagle3KVCache, load_eagle3_model
-from nanovllm_amd.engine.graphs import (ChainedProposeGraph, CommitGraph, DeviceCommitGraph,
-                                        ProposeGraph, VerifyGraph, block_table_array,
-                                        bucket_for)
+from nanovllm_amd.engine.graphs import (BUCKETS, ChainedProposeGraph, CommitGraph,
+                                        DeviceCommitGraph, ProposeGraph, VerifyGraph,
+                                        block_table_array, bucket_for)
 from nanovllm_amd.engine.sequence import Sequence
 from nanovllm_amd.layers import Attention, init_random_, param_bytes
 from nanovllm_amd.loader import load_model
@@ -140,8 +140,10 @@ class ModelRunner:
         # and the draft commit right behind the verify (DeviceCommitGraph)
         self.pipeline_verify = True
         self.device_commit = True
-        # tests: draft_override(seqs, tokens) may rewrite the device proposals
-        # tokens [k, bucket] in place before they are verified
+        # tests and benchmarks: draft_override(seqs, tokens) may rewrite the
+        # device proposals in place before they are verified (tokens [k,
+        # bucket] from a draft graph, [steps, len(seqs)] from the eager loop;
+        # column i is seqs[i])
         self.draft_override = None
         self._inflight_verify = None
         # the next step's draft queued behind a verify (propose_verify_eagle3_batch
@@ -149,10 +151,46 @@ class ModelRunner:
         # after it once collect has the results)
         self._prelaunched = None
         self.prelaunch_stats = {"queued": 0, "used": 0}
+        # pipelined steps, and those among them with a sequence proposing
+        # fewer than k drafts (close to its budget)
+        self.pipeline_stats = {"steps": 0, "ragged": 0}
         self._proposal_host = torch.empty(0, dtype=torch.int64)
         # one pinned host buffer receives argmax + accept results each verify
         self._verify_host = torch.empty(1 << 16, dtype=torch.int32, pin_memory=True)
         self._verify_dev = torch.empty(1 << 16, dtype=torch.int32, device=self.device)
+        if self.eagle3_model is not None and self._use_graphs():
+            self.capture_eagle3_graphs()
+
+    def eagle3_graph_batch_sizes(self) -> list[int]:
+        """The padded batch sizes (buckets) whose step graphs are captured at
+        initialisation: every bucket below max_num_seqs (at most 512) and the
+        one that holds max_num_seqs, as the reference captures its draft
+        step for 1, 2, 4, 8 and multiples of 16 up to max_num_seqs
+        (model_runner.py:1472-1481)."""
+        max_bs = min(self.config.max_num_seqs, BUCKETS[-1])
+        return [b for b in BUCKETS if b < max_bs] + [bucket_for(max_bs)]
+
+    @torch.inference_mode()
+    def capture_eagle3_graphs(self) -> None:
+        """Capture the speculative step's graphs for every batch bucket
+        before serving (model_runner.py:195, :1472-1523): the verify (target
+        forward, LM head, fused argmax + accept), the k-step draft, the
+        device commit behind the verify and the next step's draft behind
+        both.  Largest bucket first, so the shared attention and argmax
+        workspaces reach their final size before the smaller captures.
+        Buckets a step needs later (a batch above max_num_seqs cannot occur)
+        are captured on first use."""
+        k = self.speculative_config.num_speculative_tokens
+        for bs in reversed(self.eagle3_graph_batch_sizes()):
+            vgraph = self._verify_graphs.get(bs)
+            if vgraph is None:
+                vgraph = self._verify_graphs[bs] = VerifyGraph(self, bs, k + 1)
+            if bs not in self._propose_graphs:
+                self._propose_graphs[bs] = ProposeGraph(self, bs, k)
+            if bs not in self._device_commit_graphs:
+                self._device_commit_graphs[bs] = DeviceCommitGraph(self, vgraph)
+            if bs not in self._chained_graphs:
+                self._chained_graphs[bs] = ChainedProposeGraph(self, bs, k, vgraph)
 
     # ------------------------------------------------------------ RPC surface
 
@@ -432,6 +470,10 @@ class ModelRunner:
     # ------------------------------------------------------------ EAGLE3
 
     def get_eagle3_runtime_capabilities(self):
+        """The reference's report (model_runner.py:982-990): a paged draft
+        cache, and the batch sizes with captured draft-step graphs (here the
+        k-step draft graphs, captured at initialisation unless
+        enforce_eager)."""
         return {
             "paged_kv_cache": bool(getattr(self, "eagle3_model", None) is not None
                                    and getattr(self, "eagle_kv_cache", None) is not None),
@@ -489,6 +531,8 @@ class ModelRunner:
             if graph is None:
                 graph = self._propose_graphs[bs] = ProposeGraph(self, bs, k)
             tokens = graph.run(rows, pos, slots, ctx_lens, [seq.block_table for seq in seqs])
+            if self.draft_override is not None:
+                self.draft_override(seqs, tokens)
             table = tokens[:, :len(seqs)].cpu().tolist()
         else:
             state_rows = _pinned(rows, torch.int64).to(self.device, non_blocking=True)
@@ -516,7 +560,10 @@ class ModelRunner:
                     tokens.append(self.eagle3_model.sample_greedy(hidden))
                     if sync_each_step:
                         tokens[-1].tolist()
-            return torch.stack(tokens).cpu().tolist()
+            stacked = torch.stack(tokens)
+            if self.draft_override is not None:
+                self.draft_override(seqs, stacked)
+            return stacked.cpu().tolist()
         finally:
             reset_context()
 
@@ -600,10 +647,17 @@ class ModelRunner:
         target forward runs while the host records the proposals.  Returns
         the proposals (as propose_eagle3_batch) and leaves the verify in
         flight for collect_verify_eagle3_batch; returns None when the graphs
-        do not cover the step (ragged proposal counts near max_tokens, no
-        bucket, or graphs off), and the caller then proposes and verifies in
-        turn.  The block tables must not change in between (the drafts'
-        blocks are reserved before proposing, as in the reference).
+        do not cover the step (no bucket, or graphs off), and the caller then
+        proposes and verifies in turn.  The block tables must not change in
+        between (the drafts' blocks are reserved before proposing, as in the
+        reference).
+
+        A sequence close to its budget proposes only min(k, max_tokens -
+        completion) tokens (model_runner.py:1169-1176); the graphs still run
+        k draft steps and k + 1 verify rows for it.  Its draft steps past its
+        own limit write no K/V (slot -1), the verify rows past it are
+        ignored (row j's target depends on the tokens up to j only), and
+        collect_verify_eagle3_batch caps its accepted count at the limit.
 
         prelaunch: also queue the next step's draft (ChainedProposeGraph)
         behind this step's verify and device commit, so that it runs while
@@ -617,8 +671,10 @@ class ModelRunner:
         bs = bucket_for(b)
         pre, self._prelaunched = self._prelaunched, None
         if (not self.pipeline_verify or not self._use_graphs() or not self.use_verify_graph
-                or self.keep_verify_inputs or bs is None or k < 1 or b == 0
-                or any(seq.max_tokens - seq.num_completion_tokens < k for seq in seqs)):
+                or self.keep_verify_inputs or bs is None or k < 1 or b == 0):
+            return None
+        limits = [min(k, seq.max_tokens - seq.num_completion_tokens) for seq in seqs]
+        if min(limits) < 1:
             return None
         lens = [len(seq) for seq in seqs]
         vgraph = self._verify_graphs.get(bs)
@@ -631,7 +687,7 @@ class ModelRunner:
                 tokens = graph.tokens
                 self.prelaunch_stats["used"] += 1
         if tokens is None:
-            pos, slots, ctx_lens = self._draft_step_metadata(seqs, [k] * b, k)
+            pos, slots, ctx_lens = self._draft_step_metadata(seqs, limits, k)
             pgraph = self._propose_graphs.get(bs)
             if pgraph is None:
                 pgraph = self._propose_graphs[bs] = ProposeGraph(self, bs, k)
@@ -676,10 +732,13 @@ class ModelRunner:
                 chained.launch(state_rows, lens, vrow, [seq.block_table for seq in seqs])
                 self._prelaunched = (chained, [seq.seq_id for seq in seqs], lens, None)
                 self.prelaunch_stats["queued"] += 1
-        self._inflight_verify = (order, vgraph, verified, [seqs[i].seq_id for i in range(b)])
+        self._inflight_verify = (order, vgraph, verified, [seqs[i].seq_id for i in range(b)],
+                                 limits)
+        self.pipeline_stats["steps"] += 1
+        self.pipeline_stats["ragged"] += min(limits) < k
         proposed.synchronize()
         table = host.view(k, bs)[:, :b].tolist()
-        return [[table[s][i] for s in range(k)] for i in range(b)]
+        return [[table[s][i] for s in range(limits[i])] for i in range(b)]
 
     @torch.inference_mode()
     def collect_verify_eagle3_batch(self, seqs: list[Sequence], num_input_tokens: list[int]):
@@ -688,11 +747,11 @@ class ModelRunner:
         order, each verifying its k proposals)."""
         if self._inflight_verify is None:
             raise RuntimeError("collect_verify_eagle3_batch needs propose_verify_eagle3_batch first")
-        order, vgraph, verified, ids = self._inflight_verify
+        order, vgraph, verified, ids, limits = self._inflight_verify
         self._inflight_verify = None
-        k = self.speculative_config.num_speculative_tokens
         b = len(seqs)
-        if [seq.seq_id for seq in seqs] != ids or any(n != k + 1 for n in num_input_tokens):
+        if [seq.seq_id for seq in seqs] != ids or \
+                list(num_input_tokens) != [n + 1 for n in limits]:
             raise RuntimeError("EAGLE3 verification metadata does not match the proposed batch")
         verified.synchronize()
         bs, q, t_pad = vgraph.bs, vgraph.q, vgraph.T
@@ -700,9 +759,16 @@ class ModelRunner:
         cu = [i * q for i in range(b + 1)]
         out_t, out_a, out_b = [None] * b, [0] * b, [0] * b
         for p, i in enumerate(order):
-            out_t[i] = res[cu[p]:cu[p + 1]]
-            out_a[i] = res[t_pad + p]
-            out_b[i] = res[t_pad + bs + p]
+            # the first limit + 1 rows are the sequence's verify window; the
+            # scan over all k drafts is capped at its limit (a sequence whose
+            # cap bites reaches its budget this step)
+            n = limits[i]
+            out_t[i] = res[cu[p]:cu[p] + n + 1]
+            a = res[t_pad + p]
+            if a > n:
+                out_a[i], out_b[i] = n, out_t[i][n]
+            else:
+                out_a[i], out_b[i] = a, res[t_pad + bs + p]
         self._pending_verify = (vgraph.aux, cu, {seqs[i].seq_id: p for p, i in enumerate(order)})
         self._pending_graph = vgraph
         if self._prelaunched is not None:

@@ -32,7 +32,8 @@ def dirs(tmp_path_factory):
 def make_llm(dirs, spec=True, k=4, blocks=96, eager=True, kv_cache_dtype="auto"):
     target, draft = dirs
     kw = dict(load_format="dummy", seed=0, max_model_len=2048, num_kvcache_blocks=blocks,
-              enforce_eager=eager, max_num_batched_tokens=4096, kv_cache_dtype=kv_cache_dtype)
+              enforce_eager=eager, max_num_batched_tokens=4096, kv_cache_dtype=kv_cache_dtype,
+              max_num_seqs=16)
     if spec:
         kw["speculative_config"] = {"method": "eagle3", "model": draft,
                                     "num_speculative_tokens": k, "aux_hidden_state_layers": AUX}
@@ -188,14 +189,25 @@ def test_hip_graph_steps_are_greedy(dirs):
     sp = SamplingParams(temperature=0.0, max_tokens=33, ignore_eos=True)
     eager = make_llm(dirs, spec=True, eager=True)
     try:
+        assert eager.model_runner.get_eagle3_runtime_capabilities() == {
+            "paged_kv_cache": True, "cuda_graph": False, "graph_batch_sizes": []}
         ref = [o["token_ids"] for o in eager.generate(ps, sp, use_tqdm=False)]
     finally:
         eager.exit()
     graphed = make_llm(dirs, spec=True, eager=False)
     try:
+        # captured at initialisation, as the reference reports at engine-up
+        # (model_runner.py:195, :982-990): every bucket up to max_num_seqs
+        runner = graphed.model_runner
+        assert runner.get_eagle3_runtime_capabilities() == {
+            "paged_kv_cache": True, "cuda_graph": True, "graph_batch_sizes": [1, 2, 4, 8, 16]}
+        captured = {b: (runner._verify_graphs[b], runner._propose_graphs[b])
+                    for b in (1, 2, 4, 8, 16)}
         got = [o["token_ids"] for o in graphed.generate(ps, sp, use_tqdm=False)]
-        caps = graphed.model_runner.get_eagle3_runtime_capabilities()
-        assert caps["cuda_graph"] and caps["graph_batch_sizes"]
+        # the steps replayed the graphs captured at initialisation
+        for b, (v, p) in captured.items():
+            assert runner._verify_graphs[b] is v and runner._propose_graphs[b] is p
+        assert sorted(runner._verify_graphs) == [1, 2, 4, 8, 16]
         for p, a, b in zip(ps, got, ref):
             assert_same_greedy_path(graphed, p, a, b)
         # the engine's captures leave torch's generator usable by a caller's
@@ -264,7 +276,8 @@ def test_pipelined_verify_with_oracle_drafts(dirs):
     composed on the device): proposals rewritten on the device to the
     target's own greedy continuation, corrupted at a few positions, must give
     the target's greedy path with multi-token commits, as the sequential
-    propose-then-verify path does."""
+    propose-then-verify path does; the budgets differ per sequence, so the
+    last steps verify ragged proposal counts on the same path."""
     ps = [prompts(1, seed=17, lo=240, hi=250)[0], prompts(1, seed=18, lo=20, hi=30)[0],
           prompts(1, seed=19, lo=500, hi=510)[0], prompts(1, seed=20, lo=60, hi=70)[0]]
     max_tokens = [41, 29, 33, 26]
@@ -307,6 +320,10 @@ def test_pipelined_verify_with_oracle_drafts(dirs):
         assert calls["pipelined"] > 0
         assert stats["accepted"] > stats["steps"]          # multi-token commits happened
         assert stats["committed"] == sum(max_tokens) - len(ps)
+        # the steps where a sequence is within k tokens of its budget (it
+        # proposes fewer drafts) stay on the pipelined graph path too
+        pipe = spec.model_runner.pipeline_stats
+        assert pipe["steps"] == stats["steps"] and pipe["ragged"] > 0, pipe
     finally:
         spec.exit()
 
