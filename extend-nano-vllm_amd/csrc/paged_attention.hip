@@ -14,8 +14,11 @@
 //   * fixed (everything else): one workgroup per (kv head, sequence, query
 //     tile, key split).  For bf16 tiles of up to 32 rows eight waves share a
 //     2688-key split (wave w takes chunks w, w+8, ...) and fold their
-//     softmax states together in LDS; otherwise one wave runs a 3072-key
-//     split (both lengths follow the batch, see choose_split).
+//     softmax states together in LDS; bf16 tiles of 33-64 rows run on four
+//     waves that share each chunk through LDS, one wave per 16 query
+//     columns (paged_attention_tile_kernel); FP8 tiles of more than 32 rows
+//     run one wave per 3072-key split (the lengths follow the batch, see
+//     choose_split).
 // A sequence covered by one segment gets bf16 output directly; otherwise
 // each segment writes a normalised fp32 partial plus its log-sum-exp and
 // combine_kernel merges them.
@@ -45,6 +48,7 @@
 // column per 32-column group (16-byte bf16 stores; fp32 partials when the
 // keys are split); waves sharing a segment first park their states in LDS
 // and each finishes a quarter of head_dim.
+#include <stdio.h>
 #include <stdlib.h>
 
 #include "common.h"
@@ -722,6 +726,305 @@ paged_attention_kernel(AttnParams p) {
   if (clip_owner) clear_clipped_rows(p, q_start, q_len, q_raw, threadIdx.x, blockDim.x);
 }
 
+// ---------------------------------------------------------------- shared-tile kernel
+// Tiles of 33-64 rows (64-row verify tiles of GQA group 8 with k = 7, and the
+// prefill tiles of every geometry): WPT waves share one segment (kv head,
+// sequence, query tile, key split), wave w owning the NTW = 4 / WPT column
+// tiles 16 NTW w .. of the 64 query columns over every key of the split,
+// so each wave finishes its own columns and nothing is merged.
+//   * The workgroup loads each 32-key chunk once, cooperatively: thread t
+//     takes the 16-byte granules t, t + WPT * 64, ... of the chunk's 8 KiB
+//     of K rows and 8 KiB of V rows (eight lanes cover a 128-byte line), D
+//     chunks ahead of the one being computed, into registers.  That keeps
+//     D * 16 KiB in flight per workgroup where one wave per SIMD holding
+//     all 64 columns' accumulators had room for one chunk ahead.
+//   * A chunk's registers are written to one of two LDS slots (K rows, then
+//     V rows, 68 dwords per row: conflict-free for the 16-byte writes, the
+//     16-byte K operand reads and the V column reads), and one barrier per
+//     chunk publishes it and frees the other slot.
+//   * The query operands stay in registers (NTW column tiles per wave); the
+//     S^T, softmax and O^T steps are attend_segment's, per wave.
+// The loads of chunks past the end use an empty descriptor (zeros, no
+// memory traffic), so every step of the D-unrolled loop issues the same
+// loads and the compiler's waits only ever wait for the oldest buffer.
+template <int WPT, int D>
+__global__ void __launch_bounds__(kWave * WPT, 2)
+paged_attention_tile_kernel(AttnParams p) {
+  constexpr int NTW = 4 / WPT;
+  constexpr int kThreads = kWave * WPT;
+  constexpr int kRowGran = kD * 2 / 16;                  // 16-byte granules per K or V row
+  constexpr int kHalf = kChunk * kRowGran / kThreads;    // per thread per chunk, of K (and of V)
+  constexpr int kSlot = 2 * kChunk * kVPitch;            // dwords: K rows, then V rows
+  static_assert(WPT == 2 || WPT == 4, "two or four waves per 64-row tile");
+  __shared__ __attribute__((aligned(16))) uint32_t slots[2 * kSlot];
+
+  const int kvh = blockIdx.x;
+  const int seq = blockIdx.y;
+  const int split = blockIdx.z % p.max_splits;
+  const int qt = blockIdx.z / p.max_splits;
+  const int kv_begin = split * p.split_len;
+  const int lane_blk = split_block_ids(p, seq, kv_begin);
+  int q_start, q_len, L, q_raw;
+  seq_geometry_uniform(p, seq, q_start, q_len, L, &q_raw);
+  const int j0 = qt * p.qtile;
+  const int jn = (q_len - j0 < p.qtile) ? q_len - j0 : p.qtile;
+  const int kv_limit = L - q_len + j0 + jn;  // meaningful when jn > 0
+  const int nsplit = kv_limit > 0 ? (kv_limit + p.split_len - 1) / p.split_len : 0;
+  const bool note = kvh == 0 && split == 0 && p.row_nsplit;
+  const bool clip_owner = kvh == 0 && split == 0 && qt == p.n_qtiles - 1 && q_raw > q_len;
+  if (jn <= 0 || kv_begin >= kv_limit) {
+    if (jn > 0) {
+      if (note) note_rows(p, seq, qt, nsplit);
+      if (kv_limit <= 0 && split == 0) zero_tile(p, kvh, seq, qt);
+    }
+    if (clip_owner) clear_clipped_rows(p, q_start, q_len, q_raw, threadIdx.x, blockDim.x);
+    return;
+  }
+  if (note) note_rows(p, seq, qt, nsplit);
+  const int kv_end = kv_begin + p.split_len < kv_limit ? kv_begin + p.split_len : kv_limit;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & (kWave - 1);
+  const int wv = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int g = lane >> 4;
+  const int m16 = lane & 15;
+  const int rows = jn * p.group;
+  const float sl2 = p.scale_log2;
+
+  // ---- this wave's query operands (padding columns zero) and causal limits
+  int lim[NTW];
+  bf16x8_t qv[NTW][4];
+#pragma unroll
+  for (int nt = 0; nt < NTW; ++nt) {
+    const int n = (wv * NTW + nt) * 16 + m16;
+    const int nn = n < rows ? n : 0;
+    const int j = j0 + nn / p.group, hh = nn % p.group;
+    const uint16_t* qp = p.q + static_cast<int64_t>(q_start + j) * p.q_row_stride +
+                         static_cast<int64_t>(kvh * p.group + hh) * p.q_head_stride;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) qv[nt][s] = *reinterpret_cast<const bf16x8_t*>(qp + 32 * s + 8 * g);
+    const int c = L - q_len + j;
+    lim[nt] = n < rows ? (c < L - 1 ? c : L - 1) : -1;
+  }
+
+  const int nchunks = (kv_end - kv_begin + kChunk - 1) / kChunk;
+  const int first_blk = kv_begin / p.block_size;
+  const uint32_t tokb = static_cast<uint32_t>(p.tok_stride * 2);
+  // granule i of this thread: row (tid + i * kThreads) / 16, column % 16
+  uint32_t goff[kHalf], loff[kHalf];
+#pragma unroll
+  for (int i = 0; i < kHalf; ++i) {
+    const int gi = tid + i * kThreads;
+    goff[i] = static_cast<uint32_t>(gi / kRowGran) * tokb + (gi % kRowGran) * 16;
+    loff[i] = static_cast<uint32_t>(gi / kRowGran) * kVPitch + (gi % kRowGran) * 4;
+  }
+
+  // chunk c's block id (uniform), in range or not
+  auto chunk_block = [&](int c) {
+    const int kb = kv_begin + c * kChunk;
+    return __builtin_amdgcn_readlane(lane_blk, kb / p.block_size - first_blk);
+  };
+  auto load_chunk = [&](int c, uint4 (&r)[2 * kHalf]) {
+    const bool live = c < nchunks;
+    const int cc = live ? c : nchunks - 1;
+    const int kb = kv_begin + cc * kChunk;
+    const int raw = chunk_block(cc);
+    const bool valid = live && raw >= 0 && raw < p.num_blocks;
+    const int visible = kv_limit - kb < kChunk ? kv_limit - kb : kChunk;
+    const int nrec = valid ? visible * static_cast<int>(tokb) : 0;
+    const int64_t tile = (static_cast<int64_t>(valid ? raw : 0) * p.blk_stride +
+                          static_cast<int64_t>(kvh) * p.head_stride +
+                          static_cast<int64_t>(kb % p.block_size) * p.tok_stride) * 2;
+    const __amdgpu_buffer_rsrc_t kr = make_rsrc(p.k_cache + tile, nrec);
+    const __amdgpu_buffer_rsrc_t vr = make_rsrc(p.v_cache + tile, nrec);
+#pragma unroll
+    for (int i = 0; i < kHalf; ++i)
+      r[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(kr, goff[i], 0,
+                                                                             kLoadStreamed));
+#pragma unroll
+    for (int i = 0; i < kHalf; ++i)
+      r[kHalf + i] = __builtin_bit_cast(
+          uint4, __builtin_amdgcn_raw_buffer_load_b128(vr, goff[i], 0, kLoadStreamed));
+  };
+  auto stage = [&](const uint4 (&r)[2 * kHalf], int slot) {
+    uint32_t* kst = slots + slot * kSlot;
+#pragma unroll
+    for (int i = 0; i < kHalf; ++i) *reinterpret_cast<uint4*>(kst + loff[i]) = r[i];
+#pragma unroll
+    for (int i = 0; i < kHalf; ++i)
+      *reinterpret_cast<uint4*>(kst + kChunk * kVPitch + loff[i]) = r[kHalf + i];
+  };
+
+  float m_run[NTW], l_run[NTW];
+  f32x4_t acc[NTW][8];
+#pragma unroll
+  for (int nt = 0; nt < NTW; ++nt) {
+    m_run[nt] = -INFINITY;
+    l_run[nt] = 0.0f;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) acc[nt][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+
+  auto compute = [&](int c, int slot) {
+    const int raw = chunk_block(c);
+    if (raw < 0 || raw >= p.num_blocks) return;       // invalid block: its keys are masked
+    const int kb = kv_begin + c * kChunk;
+    const uint32_t* kst = slots + slot * kSlot;
+    const uint32_t* vst = kst + kChunk * kVPitch;
+    f32x4_t sacc[2][NTW];
+#pragma unroll
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int nt = 0; nt < NTW; ++nt) sacc[kt][nt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      bf16x8_t kop[2];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+        kop[kt] = *reinterpret_cast<const bf16x8_t*>(kst + (16 * kt + m16) * kVPitch + 16 * s + 4 * g);
+#pragma unroll
+      for (int nt = 0; nt < NTW; ++nt)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) sacc[kt][nt] = mfma(kop[kt], qv[nt][s], sacc[kt][nt]);
+    }
+    const bool full = kb + kChunk - 1 <= L - q_len + j0 && kb + kChunk <= kv_limit;
+    bf16x8_t pb[NTW];
+#pragma unroll
+    for (int nt = 0; nt < NTW; ++nt) {
+      float sv[8];
+      float cmax = -INFINITY;
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float v = sacc[kt][nt][i];
+          if (!full) v = (kb + kt * 16 + 4 * g + i <= lim[nt]) ? v : -INFINITY;
+          sv[kt * 4 + i] = v;
+          cmax = fmaxf(cmax, v);
+        }
+      }
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 16, kWave));
+      cmax = fmaxf(cmax, __shfl_xor(cmax, 32, kWave));
+      cmax *= sl2;
+      const bool need = cmax > m_run[nt] + kRescaleSlack;
+      if (__any(need)) {
+        const float m_new = need ? cmax : m_run[nt];
+        const float alpha = need ? exp2f_fast(m_run[nt] - m_new) : 1.0f;
+        l_run[nt] *= alpha;
+        m_run[nt] = m_new;
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[nt][t][i] *= alpha;
+        }
+      }
+      const float msub = m_run[nt] == -INFINITY ? 0.0f : m_run[nt];
+      float psum = 0.0f;
+      f32x2_t pv[4];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const float e = exp2f_fast(__builtin_fmaf(sv[k], sl2, -msub));
+        pv[k >> 1][k & 1] = e;
+        psum += e;
+      }
+      l_run[nt] += psum;
+      uint4 pk;
+      pk.x = __builtin_bit_cast(uint32_t, __builtin_convertvector(pv[0], bf16x2_t));
+      pk.y = __builtin_bit_cast(uint32_t, __builtin_convertvector(pv[1], bf16x2_t));
+      pk.z = __builtin_bit_cast(uint32_t, __builtin_convertvector(pv[2], bf16x2_t));
+      pk.w = __builtin_bit_cast(uint32_t, __builtin_convertvector(pv[3], bf16x2_t));
+      pb[nt] = __builtin_bit_cast(bf16x8_t, pk);
+    }
+    // O^T += V^T . P^T ; pair pp covers d = 32 pp + 2 m + {0 (even tile), 1 (odd tile)}
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) {
+      uint32_t w[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int key = (j < 4) ? (4 * g + j) : (16 + 4 * g + (j - 4));
+        w[j] = vst[key * kVPitch + 16 * pp + m16];
+      }
+      uint4 ev, od;
+      ev.x = __builtin_amdgcn_perm(w[1], w[0], 0x05040100u);
+      ev.y = __builtin_amdgcn_perm(w[3], w[2], 0x05040100u);
+      ev.z = __builtin_amdgcn_perm(w[5], w[4], 0x05040100u);
+      ev.w = __builtin_amdgcn_perm(w[7], w[6], 0x05040100u);
+      od.x = __builtin_amdgcn_perm(w[1], w[0], 0x07060302u);
+      od.y = __builtin_amdgcn_perm(w[3], w[2], 0x07060302u);
+      od.z = __builtin_amdgcn_perm(w[5], w[4], 0x07060302u);
+      od.w = __builtin_amdgcn_perm(w[7], w[6], 0x07060302u);
+      const bf16x8_t ea = __builtin_bit_cast(bf16x8_t, ev);
+      const bf16x8_t oa = __builtin_bit_cast(bf16x8_t, od);
+#pragma unroll
+      for (int nt = 0; nt < NTW; ++nt) {
+        acc[nt][2 * pp] = mfma(ea, pb[nt], acc[nt][2 * pp]);
+        acc[nt][2 * pp + 1] = mfma(oa, pb[nt], acc[nt][2 * pp + 1]);
+      }
+    }
+  };
+
+  // ---- D chunks in flight in registers, two LDS slots: step c computes
+  // chunk c from slot c & 1, stages chunk c + 1 (loaded D steps ago) into
+  // the other slot, refills its registers with chunk c + 1 + D, and one
+  // barrier publishes the staged chunk and frees slot c & 1.
+  uint4 buf[D][2 * kHalf];
+#pragma unroll
+  for (int d = 0; d < D; ++d) load_chunk(d, buf[d]);
+  stage(buf[0], 0);
+  load_chunk(D, buf[0]);
+  __syncthreads();
+  for (int cb = 0; cb < nchunks; cb += D) {
+#pragma unroll
+    for (int d = 0; d < D; ++d) {
+      const int c = cb + d;
+      if (c < nchunks) compute(c, c & 1);
+      const int nb = (d + 1) % D;          // a constant once the loop is unrolled
+      stage(buf[nb], (c + 1) & 1);
+      load_chunk(c + 1 + D, buf[nb]);
+      __syncthreads();
+    }
+  }
+
+  // ---- finish: this wave's columns, straight from registers (lane (g, m16)
+  // holds d = 32 pp + 8 g + 0..7 of query column m16 in the tiles 2 pp and
+  // 2 pp + 1)
+#pragma unroll
+  for (int nt = 0; nt < NTW; ++nt) {
+    float lsum = l_run[nt];
+    lsum += __shfl_xor(lsum, 16, kWave);
+    lsum += __shfl_xor(lsum, 32, kWave);
+    const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
+    const int n = (wv * NTW + nt) * 16 + m16;
+    if (n < rows) {
+      const int j = j0 + n / p.group, hh = n % p.group;
+      const int tok = q_start + j;
+      const int h = kvh * p.group + hh;
+      const int64_t slot = (static_cast<int64_t>(tok) * p.hq + h) * p.max_splits + split;
+#pragma unroll
+      for (int pp = 0; pp < 4; ++pp) {
+        float o[8];
+#pragma unroll
+        for (int e = 0; e < 2; ++e)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) o[2 * i + e] = acc[nt][2 * pp + e][i] * inv;
+        const int d0 = 32 * pp + 8 * g;
+        if (nsplit == 1) {
+          uint16_t* op = p.out + static_cast<int64_t>(tok) * p.out_row_stride +
+                         static_cast<int64_t>(h) * p.out_head_stride + d0;
+          *reinterpret_cast<uint4*>(op) = make_uint4(pack_bf16(o[0], o[1]), pack_bf16(o[2], o[3]),
+                                                     pack_bf16(o[4], o[5]), pack_bf16(o[6], o[7]));
+        } else {
+          float* wo = p.ws_o + slot * kD + d0;
+          *reinterpret_cast<float4*>(wo) = make_float4(o[0], o[1], o[2], o[3]);
+          *reinterpret_cast<float4*>(wo + 4) = make_float4(o[4], o[5], o[6], o[7]);
+        }
+      }
+      if (nsplit > 1 && g == 0) p.ws_lse[slot] = lsum > 0.0f ? m_run[nt] + __log2f(lsum) : -INFINITY;
+    }
+  }
+  if (clip_owner) clear_clipped_rows(p, q_start, q_len, q_raw, threadIdx.x, blockDim.x);
+}
+
 // Balanced ("stream") decomposition for one query tile per sequence (verify
 // and decode).  For each kv head, the chunks of all sequences are laid end
 // to end and cut into equal ranges of rc chunks; workgroup (kvh, r) takes
@@ -963,8 +1266,14 @@ void choose_split(int32_t num_seqs, int32_t num_kv_heads, int32_t n_qtiles, int3
 //     us, Qwen3-0.6B verify 74.4 -> 65.1 us);
 //   * single-tile sequences of up to 32 rows, FP8: stream decomposition with
 //     the chunk loads issued one chunk ahead (502 us against 573 us fixed);
-//   * 64-row tiles: fixed decomposition with the loads one chunk ahead (one
-//     wave per SIMD for 64 rows: no room for a second).
+//   * bf16 64-row tiles: the shared-tile kernel, four waves per tile with
+//     every chunk loaded once per workgroup and two or three chunks in
+//     flight (Qwen3-32B verify, config 5's shapes: 425-428 us against 477 us
+//     for one wave per SIMD holding all 64 columns and one chunk ahead;
+//     four chunks in flight 441 us, the registers then allow two waves per
+//     SIMD instead of three; two waves per tile 432 us);
+//   * FP8 64-row tiles: fixed decomposition with the loads one chunk ahead
+//     (one wave per SIMD for 64 rows: no room for a second).
 // NVA_ATTN_STREAM=0/1 (1: also bf16 tiles of up to 16 rows) and
 // NVA_ATTN_PIPE=0/1 override the choices (tuning).
 int env_choice(const char* name) {
@@ -1047,8 +1356,61 @@ size_t workspace_bytes(int32_t num_seqs, int32_t num_tokens, int32_t hq, int32_t
   return bytes;
 }
 
+// Shared-tile kernel for bf16 64-row tiles: waves per tile and chunks in
+// flight.  NVA_ATTN_TILE=0 selects the one-wave kernel instead; "W,D"
+// (W = 2 or 4, D = 2..4) picks a variant (tuning).
+struct TileChoice {
+  int wpt, depth;
+};
+TileChoice tile_choice() {
+  static const TileChoice c = [] {
+    TileChoice t{4, 3};
+    const char* v = getenv("NVA_ATTN_TILE");
+    if (v) {
+      int w = 0, d = 0;
+      if (atoi(v) == 0) return TileChoice{0, 0};
+      // two waves per tile hold 32 columns' accumulators each: only two
+      // chunks in flight fit their registers without spilling
+      if (sscanf(v, "%d,%d", &w, &d) == 2 && ((w == 2 && d == 2) || (w == 4 && d >= 2 && d <= 4)))
+        t = TileChoice{w, d};
+    }
+    return t;
+  }();
+  return c;
+}
+
+template <int WPT>
+void launch_tile(const AttnParams& p, int depth, dim3 grid, hipStream_t s) {
+  if constexpr (WPT == 2) {
+    paged_attention_tile_kernel<2, 2><<<grid, kWave * 2, 0, s>>>(p);
+    return;
+  }
+  switch (depth) {
+    case 3:
+      paged_attention_tile_kernel<WPT, 3><<<grid, kWave * WPT, 0, s>>>(p);
+      return;
+    case 4:
+      paged_attention_tile_kernel<WPT, 4><<<grid, kWave * WPT, 0, s>>>(p);
+      return;
+    default:
+      paged_attention_tile_kernel<WPT, 2><<<grid, kWave * WPT, 0, s>>>(p);
+      return;
+  }
+}
+
 template <int NT>
 void launch_nt(const AttnParams& p, bool fp8, bool stream, dim3 grid, hipStream_t s) {
+  if constexpr (NT == 4) {
+    const TileChoice t = tile_choice();
+    if (!fp8 && t.wpt == 2) {
+      launch_tile<2>(p, t.depth, grid, s);
+      return;
+    }
+    if (!fp8 && t.wpt == 4) {
+      launch_tile<4>(p, t.depth, grid, s);
+      return;
+    }
+  }
   const bool pipe = pipelined(NT, fp8);
   if constexpr (NT < 4) {
     if (stream) {
