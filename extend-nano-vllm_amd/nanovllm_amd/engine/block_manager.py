@@ -71,10 +71,14 @@ class BlockManager:
 
     # ------------------------------------------------------------ pool
 
-    def _new_page(self) -> Page:
-        """The head of the free list, emptied, with one reference.  Its old
-        key stops pointing at it."""
-        page = self.blocks[self.free_block_ids.popleft()]
+    def _new_page(self, block_id: int | None = None) -> Page:
+        """The head of the free list (or the free page ``block_id``), emptied,
+        with one reference.  Its old key stops pointing at it."""
+        if block_id is None:
+            page = self.blocks[self.free_block_ids.popleft()]
+        else:
+            self.free_block_ids.remove(block_id)
+            page = self.blocks[block_id]
         assert page.ref_count == 0
         if page.hash != NO_KEY and self.hash_to_block_id.get(page.hash) == page.block_id:
             del self.hash_to_block_id[page.hash]
@@ -212,14 +216,35 @@ class BlockManager:
 
     # ------------------------------------------------------------ speculation
 
-    def ensure_num_blocks_for_length(self, seq: Sequence, num_tokens: int) -> None:
+    # pages the look-ahead reservation searches at the free list's tail
+    LOOKAHEAD_SCAN = 64
+
+    def _lookahead_page_id(self) -> int | None:
+        """A free page for a look-ahead reservation: the newest page without
+        a key among the last LOOKAHEAD_SCAN of the free list (a truncate
+        returns the rejected positions' unkeyed pages there), so keyed
+        pages waiting for prefix reuse keep their place; None (the head)
+        when there is none."""
+        free = self.free_block_ids
+        for i, block_id in enumerate(reversed(free)):
+            if i == self.LOOKAHEAD_SCAN:
+                break
+            if self.blocks[block_id].hash == NO_KEY:
+                return block_id
+        return None
+
+    def ensure_num_blocks_for_length(self, seq: Sequence, num_tokens: int,
+                                     lookahead: bool = False) -> None:
         """Reserve pages for ``num_tokens`` tokens before the draft writes K/V
-        for positions not yet committed."""
+        for positions not yet committed.  ``lookahead`` pages (one step
+        further than the reference reserves, held only until the step's
+        truncate) come from the free list's tail, see _lookahead_page_id."""
         missing = -(-num_tokens // self.block_size) - len(seq.block_table)
         for _ in range(missing):
             if not self.free_block_ids:
                 raise RuntimeError("not enough KV-cache blocks for speculative proposal")
-            seq.block_table.append(self._new_page().block_id)
+            block_id = self._lookahead_page_id() if lookahead else None
+            seq.block_table.append(self._new_page(block_id).block_id)
 
     def truncate(self, seq: Sequence) -> None:
         """Release the pages past the sequence's current length (rejected

@@ -162,7 +162,10 @@ class Scheduler:
         sequence (len + 2k tokens, within the token budget), so that the next
         step's draft can be queued before this step's results are read.
         False, with nothing reserved, when the pool is short of pages.
-        postprocess_speculation releases what the step does not keep."""
+        postprocess_speculation releases what the step does not keep.  The
+        extra pages are unkeyed ones from the free list's tail (where the
+        step's truncate returns them), so the per-step churn leaves pages
+        that wait for prefix reuse alone."""
         bm = self.block_manager
         k = self.num_speculative_tokens
         limits = [min(seq.max_tokens + seq.num_prompt_tokens, len(seq) + 2 * k) for seq in seqs]
@@ -171,7 +174,7 @@ class Scheduler:
         if need > len(bm.free_block_ids):
             return False
         for seq, n in zip(seqs, limits):
-            bm.ensure_num_blocks_for_length(seq, n)
+            bm.ensure_num_blocks_for_length(seq, n, lookahead=True)
         return True
 
     def begin_speculation(self, seq: Sequence, proposal_tokens: list[int]) -> int:

@@ -169,6 +169,10 @@ int nva_argmax_accept(const void *logits, int64_t row_stride, int32_t vocab,
  *   NVA_ARGMAX_STATIC_KEYS 64-bit keys (512 KiB) that each GPU holds until
  *   the process ends.  Its address is looked up once per device
  *   (hipGetSymbolAddress) on the first call made with that device current.
+ *   A caller that records the call into a HIP graph makes one ordinary
+ *   (uncaptured) call on that device first, so that the lookup, a runtime
+ *   call, happens outside the capture; captured calls and their replays then
+ *   only launch kernels.
  * Limit: num_tokens * ceil(vocab / 16384) <= NVA_ARGMAX_STATIC_KEYS (6553
  *   rows of a 151936-token vocabulary); larger inputs return
  *   NVA_ERR_CAPACITY and launch nothing.  The stream must belong to the

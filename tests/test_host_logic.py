@@ -522,3 +522,40 @@ def test_sampling_params_errors_follow_the_reference():
     with pytest.raises(ValueError, match="max_tokens"):
         SamplingParams(max_tokens=0)
     assert SamplingParams(temperature=0.0, max_tokens=1).max_tokens == 1
+
+
+def test_lookahead_churn_leaves_cached_prefix_pages_alone():
+    """reserve_lookahead's extra pages are unkeyed pages from the free
+    list's tail (where the step's truncate returns them), so a finished
+    sequence's keyed prefix pages, waiting in the free list, survive
+    several look-ahead steps and a new request with the same prompt reuses
+    them.  Taking them from the head instead cycles the six-page pool in
+    five steps and evicts both."""
+    sched = _scheduler(num_blocks=6, k=5)
+    bm = sched.block_manager
+    a = _prefilled(sched, list(range(1000, 1512)), 3, max_tokens=64, ignore_eos=True)
+    keyed = list(a.block_table)
+    assert len(keyed) == 2 and all(bm.blocks[b].hash != -1 for b in keyed)
+    sched.running.remove(a)
+    bm.deallocate(a)                          # both pages wait, keyed, in the free list
+    b = _prefilled(sched, list(range(245)), 1, max_tokens=64, ignore_eos=True)
+    looked_ahead = 0
+    for step in range(8):
+        seqs, is_prefill = sched.schedule()
+        assert not is_prefill and seqs == [b]
+        sched.reserve_speculation(b)
+        before = len(b.block_table)
+        assert sched.reserve_lookahead([b])
+        looked_ahead += len(b.block_table) > before
+        base = sched.begin_speculation(b, [7, 7, 7, 7, 7])
+        b.num_computed_tokens = base - 1
+        v = verify_greedy_proposals([7, 7, 7, 7, 7], [9, 9, 9, 9, 9, 9])   # nothing accepted
+        sched.postprocess_speculation(b, base, v.accepted_tokens, v.replacement_token)
+        _check_invariants(sched, [b])
+    assert looked_ahead >= 5
+    for block_id in keyed:
+        assert block_id in bm.free_block_ids and bm.hash_to_block_id[bm.blocks[block_id].hash] == block_id
+    c = Sequence(list(range(1000, 1512)), SamplingParams(temperature=0.0, max_tokens=8))
+    hits = bm.stats["prefix_cache_hits"]
+    bm.allocate(c)
+    assert bm.stats["prefix_cache_hits"] == hits + 2 and c.block_table == keyed

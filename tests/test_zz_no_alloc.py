@@ -90,3 +90,33 @@ def test_static_entry_equals_workspace_entry_on_shrinking_calls(K, cuda):
         np.testing.assert_array_equal(st[:t], ref_am)
         np.testing.assert_array_equal(st[t:t + batch], ref_acc)
         np.testing.assert_array_equal(st[t + batch:], ref_bonus)
+
+
+def test_static_entry_under_graph_capture_and_replay(K, cuda):
+    """One ordinary call (the per-device address lookup happens there), then
+    the entry point recorded into a HIP graph and replayed: every replay,
+    with new logits copied into the captured input between replays and the
+    host's own eager work in between, equals the workspace entry point bit
+    for bit."""
+    batch, k = 64, 5
+    logits, cu_q, ids, _ = acceptance_logits(batch, k, VOCAB, 0.7, 11)
+    t = logits.shape[0]
+    x = logits.to(cuda)
+    cu_d, ids_d = cu_q.to(cuda), ids.to(cuda)
+    out = torch.full((t + 2 * batch,), -7, dtype=torch.int32, device=cuda)
+    K.argmax_accept_static(x, cu_d, ids_d, out)          # the warm-up call
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        K.argmax_accept_static(x, cu_d, ids_d, out)
+    torch.cuda.synchronize()
+    for rep in range(4):
+        fresh, _, _, _ = acceptance_logits(batch, k, VOCAB, 0.7, 100 + rep)
+        x.copy_(fresh.to(cuda))
+        out.fill_(-9)
+        g.replay()
+        want = torch.empty_like(out)
+        K.argmax_accept(x, cu_d, ids_d, out=want)        # eager, between replays
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(out.cpu().numpy(), want.cpu().numpy())
+        assert (out[t:t + batch] >= 0).all()
