@@ -1,11 +1,14 @@
 """HIP-graph captures of the three device stages of a speculative step.
 
-Each graph is captured once per padded batch size (bucket) on first use and
+Each graph is captured once per padded batch size (bucket) -- every bucket
+up to max_num_seqs when the runner is built, any other on first use -- and
 replayed with its static metadata buffers refreshed by one host->device copy
 per dtype.  Padded sequences have slot -1 (no K/V write) and block id -1 (no
-K/V read), so they cost compute but touch no cache state.  Steps the graphs
-do not cover (ragged proposal counts near max_tokens, ragged commits) run
-eagerly; results are identical either way.
+K/V read), so they cost compute but touch no cache state.  Sequences close
+to their token budget propose fewer drafts; the graphs still run k draft
+steps and k + 1 verify rows for them, with slot -1 past their own limit.
+Steps the graphs do not cover (no bucket, graphs off, ragged commits off the
+device-commit path) run eagerly; results are identical either way.
 
   VerifyGraph   target forward over q = k+1 rows per sequence, all-row LM
                 head, fused argmax + accept      (model_runner.py:1047-1078)
@@ -355,7 +358,7 @@ class ChainedProposeGraph(ProposeGraph):
         steps = max(k - 1, 1)
         dev = self.device
         if not hasattr(self, "lens"):
-            # static inputs (host copies of the batch, natural order) and outputs
+            # static inputs (host copies, one entry per column) and outputs
             self.meta = _Staging({"state": bs, "lens": bs, "vrow": bs}, torch.int64, dev)
             self.meta32 = _Staging({"bt": bs * mb}, torch.int32, dev)
             self.meta.fill("state", [0] * bs)
@@ -379,10 +382,13 @@ class ChainedProposeGraph(ProposeGraph):
         self._draft_loop(self.meta.dev_view("state"), self.cpos, self.cslots, self.cctx, bt)
 
     def launch(self, state_rows, lens, vrows, bt_rows) -> torch.Tensor:
-        """Host lists in the batch's natural order: draft-state rows, the
-        lengths before the verified step, each sequence's row in the verify
-        batch, block tables (reserved one step ahead).  Padding rows get
-        length 0 (no K/V written).  Returns tokens [k, bs] (device)."""
+        """Host lists, one entry per draft column (the engine passes the
+        verify's order, longest sequence first, so the draft's attention
+        works through its sequences in the order that balances best):
+        draft-state rows, the lengths before the verified step, each
+        column's row in the verify batch, block tables (reserved one step
+        ahead).  Padding columns get length 0 (no K/V written).  Returns
+        tokens [k, bs] (device)."""
         b, bs = len(state_rows), self.bs
         self.meta.fill("state", list(state_rows) + [0] * (bs - b))
         self.meta.fill("lens", list(lens) + [0] * (bs - b))

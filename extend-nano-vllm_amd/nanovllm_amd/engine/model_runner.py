@@ -147,8 +147,8 @@ class ModelRunner:
         self.draft_override = None
         self._inflight_verify = None
         # the next step's draft queued behind a verify (propose_verify_eagle3_batch
-        # with prelaunch): (graph, seq ids, lengths before the step, lengths
-        # after it once collect has the results)
+        # with prelaunch): (graph, seq id per draft column, lengths before the
+        # step, lengths after it once collect has the results)
         self._prelaunched = None
         self.prelaunch_stats = {"queued": 0, "used": 0}
         # pipelined steps, and those among them with a sequence proposing
@@ -530,10 +530,18 @@ class ModelRunner:
             graph = self._propose_graphs.get(bs)
             if graph is None:
                 graph = self._propose_graphs[bs] = ProposeGraph(self, bs, k)
-            tokens = graph.run(rows, pos, slots, ctx_lens, [seq.block_table for seq in seqs])
+            # columns longest sequence first (the attention's work order)
+            order = sorted(range(len(seqs)), key=lambda i: -lens[i])
+            dseqs = [seqs[i] for i in order]
+            tokens = graph.run([rows[i] for i in order], pos[:, order], slots[:, order],
+                               ctx_lens[:, order], [seq.block_table for seq in dseqs])
             if self.draft_override is not None:
-                self.draft_override(seqs, tokens)
-            table = tokens[:, :len(seqs)].cpu().tolist()
+                self.draft_override(dseqs, tokens)
+            sorted_table = tokens[:, :len(seqs)].cpu().tolist()
+            table = [[0] * len(seqs) for _ in range(k)]
+            for p, i in enumerate(order):
+                for s_ in range(k):
+                    table[s_][i] = sorted_table[s_][p]
         else:
             state_rows = _pinned(rows, torch.int64).to(self.device, non_blocking=True)
             table = self._propose_eager(seqs, state_rows, steps, pos, slots, ctx_lens, lens)
@@ -680,32 +688,43 @@ class ModelRunner:
         vgraph = self._verify_graphs.get(bs)
         if vgraph is None:
             vgraph = self._verify_graphs[bs] = VerifyGraph(self, bs, k + 1)
+        # the verify batch runs longest sequence first (verify_eagle3_batch_fused),
+        # and so does a fresh draft's: col[i] is sequence i's draft column
+        order = sorted(range(b), key=lambda i: -lens[i])
         tokens = None
         if pre is not None:
-            graph, ids_before, _, lens_after = pre
-            if graph.bs == bs and ids_before == [seq.seq_id for seq in seqs] and lens_after == lens:
+            graph, col_ids, _, col_lens_after = pre
+            col_of = {sid: p for p, sid in enumerate(col_ids)}
+            col = [col_of.get(seq.seq_id, -1) for seq in seqs]
+            if (graph.bs == bs and len(col_ids) == b and min(col) >= 0
+                    and all(col_lens_after[c] == n for c, n in zip(col, lens))):
                 tokens = graph.tokens
                 self.prelaunch_stats["used"] += 1
         if tokens is None:
-            pos, slots, ctx_lens = self._draft_step_metadata(seqs, limits, k)
+            col = [0] * b
+            for p, i in enumerate(order):
+                col[i] = p
+            dseqs = [seqs[i] for i in order]
+            pos, slots, ctx_lens = self._draft_step_metadata(dseqs, [limits[i] for i in order], k)
             pgraph = self._propose_graphs.get(bs)
             if pgraph is None:
                 pgraph = self._propose_graphs[bs] = ProposeGraph(self, bs, k)
-            tokens = pgraph.run(self._state_rows(seqs), pos, slots, ctx_lens,
-                                [seq.block_table for seq in seqs])
+            tokens = pgraph.run(self._state_rows(dseqs), pos, slots, ctx_lens,
+                                [seq.block_table for seq in dseqs])
         if self.draft_override is not None:
-            self.draft_override(seqs, tokens)
+            by_col = [None] * b
+            for i, c in enumerate(col):
+                by_col[c] = seqs[i]
+            self.draft_override(by_col, tokens)
         if self._proposal_host.numel() < k * bs:
             self._proposal_host = torch.empty(k * bs, dtype=torch.int64, pin_memory=True)
         host = self._proposal_host[:k * bs]
         host.copy_(tokens.reshape(-1), non_blocking=True)
         proposed = torch.cuda.Event()
         proposed.record()
-        # the verify batch runs longest sequence first (verify_eagle3_batch_fused);
-        # its input ids are composed inside the graph from the proposals
-        order = sorted(range(b), key=lambda i: -lens[i])
+        # the verify's input ids are composed inside the graph from the proposals
         q = k + 1
-        vgraph.run_composed([seqs[i].token_ids[-1] for i in order], order,
+        vgraph.run_composed([seqs[i].token_ids[-1] for i in order], [col[i] for i in order],
                             [lens[i] - 1 for i in order], [q] * b,
                             [seqs[i].block_table for i in order])
         t_pad = vgraph.T
@@ -723,14 +742,15 @@ class ModelRunner:
             cgraph.run([state_rows[i] for i in order])
             self._device_committed = vgraph
             if prelaunch:
+                # the next step's draft, its columns in this verify's order
+                # (longest first), column p reading verify row p's results
                 chained = self._chained_graphs.get(bs)
                 if chained is None:
                     chained = self._chained_graphs[bs] = ChainedProposeGraph(self, bs, k, vgraph)
-                vrow = [0] * b
-                for p, i in enumerate(order):
-                    vrow[i] = p
-                chained.launch(state_rows, lens, vrow, [seq.block_table for seq in seqs])
-                self._prelaunched = (chained, [seq.seq_id for seq in seqs], lens, None)
+                chained.launch([state_rows[i] for i in order], [lens[i] for i in order],
+                               list(range(b)), [seqs[i].block_table for i in order])
+                self._prelaunched = (chained, [seqs[i].seq_id for i in order],
+                                     [lens[i] for i in order], None)
                 self.prelaunch_stats["queued"] += 1
         self._inflight_verify = (order, vgraph, verified, [seqs[i].seq_id for i in range(b)],
                                  limits)
@@ -738,7 +758,7 @@ class ModelRunner:
         self.pipeline_stats["ragged"] += min(limits) < k
         proposed.synchronize()
         table = host.view(k, bs)[:, :b].tolist()
-        return [[table[s][i] for s in range(limits[i])] for i in range(b)]
+        return [[table[s][col[i]] for s in range(limits[i])] for i in range(b)]
 
     @torch.inference_mode()
     def collect_verify_eagle3_batch(self, seqs: list[Sequence], num_input_tokens: list[int]):
@@ -772,10 +792,11 @@ class ModelRunner:
         self._pending_verify = (vgraph.aux, cu, {seqs[i].seq_id: p for p, i in enumerate(order)})
         self._pending_graph = vgraph
         if self._prelaunched is not None:
-            # the lengths the queued draft assumed: len + accepted + 1
-            graph, ids_before, lens_before, _ = self._prelaunched
-            self._prelaunched = (graph, ids_before, lens_before,
-                                 [n + a + 1 for n, a in zip(lens_before, out_a)])
+            # the lengths the queued draft assumed, per column (column p is
+            # verify row p, sequence order[p]): len + accepted + 1
+            graph, col_ids, col_lens, _ = self._prelaunched
+            self._prelaunched = (graph, col_ids, col_lens,
+                                 [n + out_a[i] + 1 for n, i in zip(col_lens, order)])
         return out_t, out_a, out_b
 
     def _verify_fused(self, seqs: list[Sequence], num_input_tokens: list[int]):

@@ -427,7 +427,10 @@ def test_prelaunched_drafts_equal_fresh_drafts(dirs):
         def override(seqs, tokens):
             k = tokens.shape[0]
             host = tokens.cpu()
-            raw.append(host[:, :len(seqs)].clone())
+            # per sequence: the two engines may order the draft columns
+            # differently (a queued draft keeps the previous verify's order)
+            raw.append({tuple(seq.prompt_token_ids): host[:, i].clone()
+                        for i, seq in enumerate(seqs)})
             for i, seq in enumerate(seqs):
                 want = full[tuple(seq.prompt_token_ids)][len(seq):len(seq) + k]
                 calls["n"] += 1
@@ -460,7 +463,9 @@ def test_prelaunched_drafts_equal_fresh_drafts(dirs):
     assert got_on == got_off
     assert len(raw_on) == len(raw_off)
     for step, (a, b) in enumerate(zip(raw_on, raw_off)):
-        assert torch.equal(a, b), step
+        assert a.keys() == b.keys(), step
+        for key in a:
+            assert torch.equal(a[key], b[key]), step
 
 
 def test_prelaunched_drafts_with_the_device_running_behind(dirs, monkeypatch):
@@ -497,7 +502,9 @@ def test_prelaunched_drafts_with_the_device_running_behind(dirs, monkeypatch):
 
         def override(seqs, tokens):
             k, bs = tokens.shape
-            raw.append(tokens[:, :len(seqs)].clone())          # stays on the device
+            # stays on the device; keyed per sequence (column orders may differ)
+            raw.append(([tuple(seq.prompt_token_ids) for seq in seqs],
+                        tokens[:, :len(seqs)].clone()))
             want = torch.zeros(k, bs, dtype=torch.int64, pin_memory=True)
             for i, seq in enumerate(seqs):
                 cont = full[tuple(seq.prompt_token_ids)][len(seq):len(seq) + k]
@@ -525,7 +532,8 @@ def test_prelaunched_drafts_with_the_device_running_behind(dirs, monkeypatch):
             runner = llm.model_runner
             waits = sum(g.i64.waits for g in runner._device_commit_graphs.values())
             waits += sum(g.meta.waits + g.meta32.waits for g in runner._chained_graphs.values())
-            return ([outs[i] for i in sorted(outs)], [r.cpu() for r in raw],
+            per_seq = [{key: t[:, i].cpu() for i, key in enumerate(keys)} for keys, t in raw]
+            return ([outs[i] for i in sorted(outs)], per_seq,
                     dict(llm.spec_stats), dict(runner.prelaunch_stats), waits)
         finally:
             llm.exit()
@@ -539,4 +547,6 @@ def test_prelaunched_drafts_with_the_device_running_behind(dirs, monkeypatch):
     assert got_on == got_off
     assert len(raw_on) == len(raw_off)
     for step, (a, b) in enumerate(zip(raw_on, raw_off)):
-        assert torch.equal(a, b), step
+        assert a.keys() == b.keys(), step
+        for key in a:
+            assert torch.equal(a[key], b[key]), step
