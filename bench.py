@@ -46,19 +46,19 @@ DEFAULT_GEMM_TUNING = os.path.join(ROOT, "extend-nano-vllm_amd", "nanovllm_amd",
 # --pmc runs of `bench.py --attention-only --roofline-repeats 2` (FETCH_SIZE,
 # then WRITE_SIZE; KiB per dispatch, mean of the 75 calls), scaled by what
 # the same counters read for a 1 GiB device copy and a 1 GiB read in the same
-# runs: FETCH_SIZE 524303 / 524348 KiB (x2.0 to bytes read), WRITE_SIZE
-# 1048576 KiB for the copy (x1.0).  Attention kernel: FETCH 158670.2, WRITE
-# 3072.0 (no sequence of this workload needs a second split, so no combine
-# kernel runs).  A recorded constant, quoted only for the default workload,
+# runs: FETCH_SIZE 524302 / 524348 KiB (x2.0 to bytes read), WRITE_SIZE
+# 1048576 KiB for the copy (x1.0).  Attention kernel (paired mode, one
+# split per sequence, so no combine kernel runs): FETCH 158667.4, WRITE
+# 3072.3.  A recorded constant, quoted only for the default workload,
 # whose shapes it was measured on, and only while the kernel source is the
 # one it was measured on.
-PMC_TRAFFIC_BYTES = int((158670.2 * 2.0 + 3072.0 * 1.0) * 1024)
+PMC_TRAFFIC_BYTES = int((158667.4 * 2.0 + 3072.3 * 1.0) * 1024)
 PMC_WORKLOAD = dict(preset="qwen3-8b", batch=64, k=5, prompt_min=256, prompt_max=2048,
                     max_tokens=256, seed=2, kv_layout="head_major")
 # the kernel source the counters were read on (sha256 of csrc/paged_attention.hip
 # then csrc/common.h, first 16 hex digits): the constant is quoted only while
 # the source is unchanged, since a change of the kernel's loads changes it
-PMC_ATTENTION_SOURCE = "fb4b789eb5a00bdc"
+PMC_ATTENTION_SOURCE = "d1374ae32cdce848"
 ATTENTION_SOURCES = ("paged_attention.hip", "common.h")
 
 

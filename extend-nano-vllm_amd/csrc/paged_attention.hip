@@ -14,7 +14,10 @@
 //   * fixed (everything else): one workgroup per (kv head, sequence, query
 //     tile, key split).  For bf16 tiles of up to 32 rows eight waves share a
 //     2688-key split (wave w takes chunks w, w+8, ...) and fold their
-//     softmax states together in LDS; bf16 tiles of 33-64 rows run on four
+//     softmax states together in LDS; for single-tile 17-32-row tiles whose
+//     segments fill every CU once or twice, four waves share a whole
+//     sequence instead and the grid pairs a long sequence with a short one
+//     on each CU (paired mode, see paired_mode); bf16 tiles of 33-64 rows run on four
 //     waves that share each chunk through LDS, one wave per 16 query
 //     columns (paged_attention_tile_kernel); FP8 tiles of more than 32 rows
 //     run one wave per 3072-key split (the lengths follow the batch, see
@@ -102,9 +105,49 @@ struct AttnParams {
   // stream decomposition (one query tile per sequence)
   int32_t min_range_chunks, max_range_chunks;
   int32_t* row_nsplit;                                // [num_tokens] split count per query row
+  // paired mode: grid rows y >= pair_rows take the sequences from the last
+  // one backwards (0: row y is sequence y)
+  int32_t pair_rows;
 };
 
 __device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Reductions over the lane pairs (l, l ^ 16) and (l, l ^ 32), every lane
+// receiving the pair's result.  gfx950's v_permlane16_swap /
+// v_permlane32_swap with both operands x leave the pair's two values, the
+// lower lane's first, in the two results of every lane of the pair: a
+// VALU exchange.  __shfl_xor compiles to ds_bpermute, which goes through
+// the LDS unit and makes the next use wait for every outstanding LDS
+// operation of the wave (in the key loop: the V rows just staged).  Both
+// lanes combine the same two values in the same order, and max and + are
+// commutative, so the results equal the shuffle forms' bit for bit.  The
+// two results are read into integers before the bit cast: a bit cast of
+// the second element of the builtin's result vector compiles to the first
+// element (ROCm 7.2 clang).
+__device__ __forceinline__ float max_xor16(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const uint32_t lo = r[0], hi = r[1];
+  return fmaxf(__builtin_bit_cast(float, lo), __builtin_bit_cast(float, hi));
+}
+__device__ __forceinline__ float max_xor32(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const uint32_t lo = r[0], hi = r[1];
+  return fmaxf(__builtin_bit_cast(float, lo), __builtin_bit_cast(float, hi));
+}
+__device__ __forceinline__ float sum_xor16(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const uint32_t lo = r[0], hi = r[1];
+  return __builtin_bit_cast(float, lo) + __builtin_bit_cast(float, hi);
+}
+__device__ __forceinline__ float sum_xor32(float x) {
+  const uint32_t u = __builtin_bit_cast(uint32_t, x);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const uint32_t lo = r[0], hi = r[1];
+  return __builtin_bit_cast(float, lo) + __builtin_bit_cast(float, hi);
+}
 
 // Orders a wave's own LDS writes and reads: LDS executes one wave's
 // operations in issue order, so the compiler must only keep program order
@@ -404,8 +447,8 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
           cmax = fmaxf(cmax, v);
         }
       }
-      cmax = fmaxf(cmax, __shfl_xor(cmax, 16, kWave));
-      cmax = fmaxf(cmax, __shfl_xor(cmax, 32, kWave));
+      cmax = max_xor16(cmax);
+      cmax = max_xor32(cmax);
       cmax *= sl2;
       const bool need = cmax > m_run[nt] + kRescaleSlack;
       if (__any(need)) {
@@ -549,8 +592,8 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
         fw[w] = fw[w] == -INFINITY ? 0.0f : exp2f_fast(fw[w] - M);
         lsum += fw[w] * st[w][kAccWords + kWave + lane];
       }
-      lsum += __shfl_xor(lsum, 16, kWave);
-      lsum += __shfl_xor(lsum, 32, kWave);
+      lsum = sum_xor16(lsum);
+      lsum = sum_xor32(lsum);
       const float inv = lsum > 0.0f ? vscale / lsum : 0.0f;
       const int n = nt * 16 + m16;
       if (n < rows) {
@@ -596,8 +639,8 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     float lsum = l_run[nt];
-    lsum += __shfl_xor(lsum, 16, kWave);
-    lsum += __shfl_xor(lsum, 32, kWave);
+    lsum = sum_xor16(lsum);
+    lsum = sum_xor32(lsum);
     const float inv = lsum > 0.0f ? vscale / lsum : 0.0f;
     const int n = nt * 16 + m16;
     if (n < rows) {
@@ -695,7 +738,8 @@ paged_attention_kernel(AttnParams p) {
   __shared__ __attribute__((aligned(16))) uint32_t vst[kVStage * WPS * (WPS > 1 && NT > 1 ? NT : 1)];
   __shared__ bf16x8_t qst[NT * 4 * kWave];
   const int kvh = blockIdx.x;
-  const int seq = blockIdx.y;
+  const int row = blockIdx.y;
+  const int seq = (p.pair_rows > 0 && row >= p.pair_rows) ? p.num_seqs - 1 - (row - p.pair_rows) : row;
   const int split = blockIdx.z % p.max_splits;
   const int qt = blockIdx.z / p.max_splits;
   const int kv_begin = split * p.split_len;
@@ -903,8 +947,8 @@ paged_attention_tile_kernel(AttnParams p) {
           cmax = fmaxf(cmax, v);
         }
       }
-      cmax = fmaxf(cmax, __shfl_xor(cmax, 16, kWave));
-      cmax = fmaxf(cmax, __shfl_xor(cmax, 32, kWave));
+      cmax = max_xor16(cmax);
+      cmax = max_xor32(cmax);
       cmax *= sl2;
       const bool need = cmax > m_run[nt] + kRescaleSlack;
       if (__any(need)) {
@@ -991,8 +1035,8 @@ paged_attention_tile_kernel(AttnParams p) {
 #pragma unroll
   for (int nt = 0; nt < NTW; ++nt) {
     float lsum = l_run[nt];
-    lsum += __shfl_xor(lsum, 16, kWave);
-    lsum += __shfl_xor(lsum, 32, kWave);
+    lsum = sum_xor16(lsum);
+    lsum = sum_xor32(lsum);
     const float inv = lsum > 0.0f ? 1.0f / lsum : 0.0f;
     const int n = (wv * NTW + nt) * 16 + m16;
     if (n < rows) {
@@ -1295,7 +1339,8 @@ bool pipelined(int nt, bool fp8) {
 
 // Waves sharing one split of the fixed decomposition.  Eight for bf16 tiles
 // of up to 32 rows without the one-chunk-ahead loads (two waves per SIMD;
-// the eight parked states fill most of the CU's LDS); one otherwise.
+// the eight parked states fill most of the CU's LDS; four in paired mode);
+// one otherwise.
 // NVA_ATTN_WPS=1/2/4/8 overrides it for those tiles (tuning).
 int segment_waves(int nt, bool fp8) {
   if (fp8 || nt >= 4 || pipelined(nt, fp8)) return 1;
@@ -1308,6 +1353,36 @@ int segment_waves(int nt, bool fp8) {
 }
 
 int tile_mfmas(int32_t tile_rows) { return tile_rows <= 16 ? 1 : tile_rows <= 32 ? 2 : 4; }
+
+// Paired mode, for bf16 single-tile sequences of 17-32 rows (the verify of
+// a GQA group of 4 with k = 4..7) whose segments number more than one and at
+// most two per CU: four waves share a whole sequence (no split, no fp32
+// partials), two such workgroups fit a CU at once (186 VGPRs, 76 KiB of
+// LDS), so every segment is resident from the start, and the grid pairs
+// them: the dispatcher gives workgroup i and workgroup i + CUs the same CU,
+// so grid rows past CUs / Hkv take the sequences from the last one
+// backwards.  With the batch longest first (the engine's verify order)
+// each CU then holds a long and a short sequence, about the same keys per
+// CU, and one workgroup's fold overlaps the other's loads.  With eight
+// waves per split (one workgroup per CU, two rounds) a CU streams nothing
+// while a workgroup folds its eight states and the next one starts.
+// Measured on config 3's shapes (B64 q6 32/8, keys U[256, 2304], 300-launch
+// graph bursts, alternating runs on one box): 56.6 against 58.0 us with
+// eight waves per 2688-key split (56.0-56.2 against 57.2-57.4 on another
+// box); without the pairing (rows in batch order) 61.6 us; the same mode
+// for 4- and 10-row tiles: no gain (53.1 against 53.0 us) and a loss
+// (62-66 against 56.1 us, 256 segments).
+// Up to kPairedMaxKeys keys per sequence (the shapes measured);
+// NVA_ATTN_PAIRED=0/1 overrides the choice (tuning).
+constexpr int32_t kPairedMaxKeys = 3072;
+bool paired_mode(int32_t num_seqs, int32_t hkv, int32_t n_qtiles, int32_t max_k, int nt, bool fp8) {
+  static const int forced = env_choice("NVA_ATTN_PAIRED");
+  if (forced == 0 || fp8 || nt != 2 || n_qtiles != 1 || pipelined(nt, fp8)) return false;
+  if (max_k > kPairedMaxKeys) return false;
+  const int64_t segs = static_cast<int64_t>(num_seqs) * hkv;
+  const int64_t cus = device_cus();
+  return segs > (forced == 1 ? 0 : cus) && segs <= 2 * cus;
+}
 
 // Upper bound on a sequence's split count in stream mode: a range holds at
 // least kMinRangeChunks chunks, and a sequence may start mid-range.
@@ -1399,7 +1474,7 @@ void launch_tile(const AttnParams& p, int depth, dim3 grid, hipStream_t s) {
 }
 
 template <int NT>
-void launch_nt(const AttnParams& p, bool fp8, bool stream, dim3 grid, hipStream_t s) {
+void launch_nt(const AttnParams& p, bool fp8, bool stream, int wps, dim3 grid, hipStream_t s) {
   if constexpr (NT == 4) {
     const TileChoice t = tile_choice();
     if (!fp8 && t.wpt == 2) {
@@ -1436,7 +1511,7 @@ void launch_nt(const AttnParams& p, bool fp8, bool stream, dim3 grid, hipStream_
     return;
   }
   if constexpr (NT < 4) {
-    switch (fp8 ? 1 : segment_waves(NT, false)) {
+    switch (fp8 ? 1 : wps) {
       case 2:
         paged_attention_kernel<NT, false, false, 2><<<grid, 2 * kWave, 0, s>>>(p);
         return;
@@ -1477,8 +1552,16 @@ int run_attention(AttnParams& p, int kv_dtype, void* workspace, size_t workspace
     return NVA_ERR_UNSUPPORTED;
   const bool fp8 = kv_dtype == NVA_KV_FP8_E4M3;
   const bool stream = stream_mode(p.num_seqs, p.max_q, p.qtile, p.group, fp8);
+  const int nt = tile_mfmas(tile_rows);
+  // paired mode's whole-sequence split must fit the kernel's block ids
+  const int32_t mk = p.max_k > 1 ? p.max_k : 1;
+  const int32_t whole = (mk + kMinSplit - 1) / kMinSplit * kMinSplit;
+  const bool paired = !stream && paired_mode(p.num_seqs, p.hkv, p.n_qtiles, p.max_k, nt, fp8) &&
+                      whole / p.block_size + 2 <= kWave;
+  int wps = segment_waves(nt, fp8);
   dim3 grid;
   p.row_nsplit = nullptr;
+  p.pair_rows = 0;
   if (stream) {
     // a range may span at most kWave - 2 whole blocks (one block id per lane)
     p.min_range_chunks = kMinRangeChunks;
@@ -1486,9 +1569,16 @@ int run_attention(AttnParams& p, int kv_dtype, void* workspace, size_t workspace
     p.max_splits = stream_max_splits(p.max_k);
     p.split_len = 0;
     grid = dim3(p.hkv, stream_ranges_per_head(p.hkv), 1);
+  } else if (paired) {
+    // one split per sequence (a multiple of 128 keys covering max_k)
+    wps = 4;
+    p.split_len = whole;
+    p.max_splits = 1;
+    p.pair_rows = device_cus() / p.hkv;
+    grid = dim3(p.hkv, p.num_seqs, p.n_qtiles);
   } else {
-    choose_split(p.num_seqs, p.hkv, p.n_qtiles, p.max_k, segment_waves(tile_mfmas(tile_rows), fp8),
-                 p.block_size, &p.split_len, &p.max_splits);
+    choose_split(p.num_seqs, p.hkv, p.n_qtiles, p.max_k, wps, p.block_size, &p.split_len,
+                 &p.max_splits);
     // the kernel keeps one block id per lane: a split may touch at most kWave blocks
     if (p.split_len / p.block_size + 2 > kWave) return NVA_ERR_UNSUPPORTED;
     grid = dim3(p.hkv, p.num_seqs, p.max_splits * p.n_qtiles);
@@ -1508,13 +1598,12 @@ int run_attention(AttnParams& p, int kv_dtype, void* workspace, size_t workspace
     p.ws_o = nullptr;
     p.ws_lse = nullptr;
   }
-  const int nt = tile_mfmas(tile_rows);
   if (nt <= 1)
-    launch_nt<1>(p, fp8, stream, grid, s);
+    launch_nt<1>(p, fp8, stream, wps, grid, s);
   else if (nt == 2)
-    launch_nt<2>(p, fp8, stream, grid, s);
+    launch_nt<2>(p, fp8, stream, wps, grid, s);
   else
-    launch_nt<4>(p, fp8, stream, grid, s);
+    launch_nt<4>(p, fp8, stream, wps, grid, s);
   if (hipGetLastError() != hipSuccess) return NVA_ERR_LAUNCH;
   if (stream || p.max_splits > 1) {
     const int slices = p.hq * (kD / 4);

@@ -32,7 +32,7 @@ def test_config3_geometry_spec_equals_target_greedy(dirs):
     def make_llm(spec):
         # the whole batch prefills in one step, so every decode step holds
         # all 64 sequences (the bench's shape)
-        kw = dict(load_format="dummy", seed=0, max_model_len=4096, num_kvcache_blocks=720,
+        kw = dict(load_format="dummy", seed=0, max_model_len=2304, num_kvcache_blocks=720,
                   enforce_eager=False, max_num_batched_tokens=131072, max_num_seqs=BATCH,
                   enable_prefill_batching=True)
         if spec:

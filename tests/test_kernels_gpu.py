@@ -776,6 +776,12 @@ def test_rms_norm_into_strided_halves(K, cuda):
 # ---------------------------------------------------------------- K1 at full BASELINE sizes
 
 FULL_CASES = {
+    # BASELINE config 3's verify: B64, q6, 32/8 heads, L ~ U[256, 2304]: 24-row
+    # tiles in paired mode (four waves per whole sequence, grid rows past
+    # CUs / Hkv taking the sequences from the last one backwards)
+    "config3": dict(seed=2, batch=64, q_len=6, ctx_lo=256, ctx_hi=2304, hq=32, hkv=8),
+    # paired mode with part of the CUs holding one segment (320 segments)
+    "config3_b40": dict(seed=12, batch=40, q_len=6, ctx_lo=256, ctx_hi=2304, hq=32, hkv=8),
     # FP8 pages, B128, q5, 16/8 heads, L ~ U[4096, 16384]
     "config4_fp8": dict(seed=3, batch=128, q_len=5, ctx_lo=4096, ctx_hi=16384, hq=16, hkv=8,
                         fp8=True),
@@ -879,7 +885,8 @@ def _picks(c, count, seed):
 @pytest.mark.parametrize("name", list(FULL_CASES))
 def test_full_size_verify_matches_oracle_on_sampled_sequences(K, cuda, name):
     """At the BASELINE configs' full sizes the whole batch runs on the GPU in
-    one launch (config 4: FP8 pages, stream ranges over 128 sequences of
+    one launch (config 3: 24-row tiles in paired mode, 64 and 40 sequences;
+    config 4: FP8 pages, stream ranges over 128 sequences of
     4096-16384 keys; config 5: 64-row tiles, splits of three quarters of
     the longest sequence (6144 keys) and the combine, the first 30% of
     every sequence's blocks shared), and the
@@ -899,8 +906,8 @@ def test_full_size_verify_matches_oracle_on_sampled_sequences(K, cuda, name):
                                    k_scale=one, v_scale=one)
     torch.cuda.synchronize()
     picks = _picks(c, 8, seed=5)
-    if not fp8:
-        # config 5: at least one sampled sequence is split (and combined)
+    if name == "config5":
+        # at least one sampled sequence is split (and combined)
         assert max(c["lens"][i] for i in picks) > 6144
     kb, vb, sub_bt, rows, qb, lens = _sample_rows(c, picks)
     q_len = c["q_len"]
