@@ -398,6 +398,31 @@ def test_verify_attention_small_pages(K, cuda, block_size, name, kw, fp8):
     assert err <= ATTN_TOL, (name, block_size, err)
 
 
+@pytest.mark.parametrize("name,kw", [
+    # paired mode (17-32-row single tiles, more than one and at most two
+    # (sequence, kv head) pairs per CU of a 256-CU device): grid rows past
+    # CUs / Hkv take the sequences from the last one backwards
+    ("hkv4_b100", dict(seed=40, batch=100, q_len=6, ctx_lo=20, ctx_hi=400, hq=16, hkv=4)),
+    # 264 pairs: a single reversed row, which maps to itself
+    ("b33_q5", dict(seed=41, batch=33, q_len=5, ctx_lo=30, ctx_hi=500, hq=32, hkv=8)),
+    ("ragged_b40", dict(seed=42, batch=40, q_len=[1, 7, 3, 6, 2, 5, 4, 7] * 5, ctx_lo=1,
+                        ctx_hi=600, hq=32, hkv=8)),
+    # whole-sequence splits up to the mode's 3072-key bound
+    ("long_b36", dict(seed=43, batch=36, q_len=6, ctx_lo=2900, ctx_hi=3072, hq=32, hkv=8)),
+    # 32-token pages: a whole-sequence split would span more pages than a
+    # wave holds block ids, so the launch falls back to eight-wave splits
+    ("pages32_b40", dict(seed=44, batch=40, q_len=6, ctx_lo=2000, ctx_hi=3000, hq=32, hkv=8,
+                         block_size=32)),
+])
+def test_verify_attention_paired_geometries(K, cuda, name, kw):
+    """The paired decomposition's row mapping and its fallback, against the
+    oracle, on batches in drawn order (the mapping is a permutation of the
+    sequences whatever their order)."""
+    got, ref = _run_verify(K, cuda, paged_case(**kw))
+    err = np.abs(got - ref).max()
+    assert err <= ATTN_TOL, (name, err)
+
+
 def test_verify_attention_fp8(K, cuda):
     case = paged_case(seed=7, batch=8, q_len=5, ctx_lo=300, ctx_hi=3000, hq=16, hkv=8)
     got, ref = _run_verify(K, cuda, case, fp8=True)
