@@ -46,13 +46,14 @@ DEFAULT_GEMM_TUNING = os.path.join(ROOT, "extend-nano-vllm_amd", "nanovllm_amd",
 # --pmc runs of `bench.py --attention-only --roofline-repeats 2` (FETCH_SIZE,
 # then WRITE_SIZE; KiB per dispatch, mean of the 75 calls), scaled by what
 # the same counters read for a 1 GiB device copy and a 1 GiB read in the same
-# runs: FETCH_SIZE 524302 / 524348 KiB (x2.0 to bytes read), WRITE_SIZE
+# runs: FETCH_SIZE 524303 / 524348 KiB (x2.0 to bytes read), WRITE_SIZE
 # 1048576 KiB for the copy (x1.0).  Attention kernel (paired mode, one
-# split per sequence, so no combine kernel runs): FETCH 158667.4, WRITE
-# 3072.3.  A recorded constant, quoted only for the default workload,
+# split per sequence, so no combine kernel runs) on the sequences of the
+# default run's roofline step (sum L = 77 172): FETCH 155979.2, WRITE
+# 3072.4.  A recorded constant, quoted only for the default workload,
 # whose shapes it was measured on, and only while the kernel source is the
 # one it was measured on.
-PMC_TRAFFIC_BYTES = int((158667.4 * 2.0 + 3072.3 * 1.0) * 1024)
+PMC_TRAFFIC_BYTES = int((155979.2 * 2.0 + 3072.4 * 1.0) * 1024)
 PMC_WORKLOAD = dict(preset="qwen3-8b", batch=64, k=5, prompt_min=256, prompt_max=2048,
                     max_tokens=256, seed=2, kv_layout="head_major")
 # the kernel source the counters were read on (sha256 of csrc/paged_attention.hip
@@ -328,7 +329,11 @@ def attention_only(args) -> None:
     g = torch.Generator().manual_seed(args.seed)
     lens = torch.randint(args.prompt_min, args.prompt_max + 1, (args.batch,), generator=g).tolist()
     lens = sorted(lens, reverse=True)  # the engine verifies its batch longest sequence first
-    done = args.warmup + args.steps + 2  # tokens each sequence holds when the roofline step runs
+    # the roofline step's position: the prompts prefilled again (one token),
+    # the warm-up steps, the profiled steps and the CPU baseline's step
+    # commit one token each (nothing is accepted), and the step verifies
+    # from the last of them: its keys are prompt + done + k + 1
+    done = args.warmup + args.profile_steps + (0 if args.no_cpu_baseline else 1)
     q_len = args.k + 1
     seqlens = [L + done + q_len for L in lens]
     block = 256
