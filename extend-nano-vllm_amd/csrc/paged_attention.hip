@@ -1307,7 +1307,8 @@ void choose_split(int32_t num_seqs, int32_t num_kv_heads, int32_t n_qtiles, int3
 //     per workgroup sharing each split (their states merged in LDS), two
 //     waves per SIMD hiding each other's latency.  This beat the stream
 //     decomposition for 4- and 10-row tiles too (draft decode 80.8 -> 70.7
-//     us, Qwen3-0.6B verify 74.4 -> 65.1 us);
+//     us, Qwen3-0.6B verify 74.4 -> 65.1 us).  Single tiles of 17-32 rows
+//     at one to two segments per CU run paired mode instead (paired_mode);
 //   * single-tile sequences of up to 32 rows, FP8: stream decomposition with
 //     the chunk loads issued one chunk ahead (502 us against 573 us fixed);
 //   * bf16 64-row tiles: the shared-tile kernel, four waves per tile with
