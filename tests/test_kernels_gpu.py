@@ -423,6 +423,31 @@ def test_verify_attention_paired_geometries(K, cuda, name, kw):
     assert err <= ATTN_TOL, (name, err)
 
 
+def test_verify_attention_paired_with_empty_padding_sequences(K, cuda):
+    """A verify graph's bucket pads the batch with empty sequences (no query
+    rows, no keys) after the real ones; in paired mode those take grid rows
+    among the reversed ones.  40 real sequences of 24-row tiles padded to
+    64 (512 (sequence, kv head) pairs): the real rows against the oracle."""
+    case = paged_case(seed=45, batch=40, q_len=6, ctx_lo=50, ctx_hi=1500, hq=32, hkv=8)
+    pad = 24
+    cu_q = torch.cat([case["cu_q"], case["cu_q"][-1:].repeat(pad)])
+    cu_k = torch.cat([case["cu_k"], case["cu_k"][-1:].repeat(pad)])
+    bt = torch.cat([case["block_tables"],
+                    torch.full((pad, case["block_tables"].shape[1]), -1, dtype=torch.int32)])
+    kc, vc = case["k_cache"].to(cuda), case["v_cache"].to(cuda)
+    K.store_kvcache(case["k_new"].to(cuda), case["v_new"].to(cuda), kc, vc,
+                    case["slot_mapping"].to(cuda), None, None)
+    out = K.paged_attention_varlen(case["q"].to(cuda), kc, vc, cu_q.to(cuda), cu_k.to(cuda), 6,
+                                   int(case["lens"].max()), 128 ** -0.5, bt.to(cuda))
+    torch.cuda.synchronize()
+    rk, rv = bits(case["k_cache"]).copy(), bits(case["v_cache"]).copy()
+    oracle.store_kv(bits(case["k_new"]), bits(case["v_new"]), rk, rv, case["slot_mapping"].numpy())
+    ref = oracle.paged_attention(bits(case["q"]), rk, rv, case["cu_q"].numpy(),
+                                 case["lens"].numpy(), case["block_tables"].numpy(), 128 ** -0.5)
+    err = np.abs(out.float().cpu().numpy() - ref).max()
+    assert err <= ATTN_TOL, err
+
+
 def test_verify_attention_fp8(K, cuda):
     case = paged_case(seed=7, batch=8, q_len=5, ctx_lo=300, ctx_hi=3000, hq=16, hkv=8)
     got, ref = _run_verify(K, cuda, case, fp8=True)
