@@ -228,6 +228,21 @@ __device__ __forceinline__ int split_block_ids(const AttnParams& p, int seq, int
   return col < p.bt_cols ? p.block_tables[static_cast<int64_t>(seq) * p.bt_stride + col] : -1;
 }
 
+// Segments over an FP8 cache, and shared segments over a bf16 cache
+// (several waves, one chunk buffer), also stage K through a wave-private
+// LDS tile: the K rows then load like the V rows, whole 128-byte lines per
+// instruction with the non-temporal hint (FP8 rows dequantised to bf16 on
+// the way in, as V's), and the MFMA operands are read back in the order
+// the registers held them.
+// NVA_K_STAGE=0 at build time keeps K in registers (half lines, default
+// policy) for comparison.
+#ifndef NVA_K_STAGE
+#define NVA_K_STAGE 1
+#endif
+constexpr bool k_staged(bool fp8, bool pipe, int wps) {
+  return NVA_K_STAGE && (fp8 || (!pipe && wps > 1));
+}
+
 // One segment of work: the query tile qt of sequence seq (all its rows
 // for kv head kvh; the sequence's rows start at q_start, it has q_len query
 // rows and L keys) against keys [kv_begin, kv_end), which is split `split`
@@ -249,11 +264,13 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
   static_assert(WPS == 1 || !PIPE, "shared segments use the single-buffer loop");
   static_assert(WPS == 1 || (NT <= 2 && (8 * kWave * 4 + 2 * kWave) <= kVStage),
                 "a wave's parked state must fit one V stage per column tile");
+  constexpr bool KST = k_staged(FP8, PIPE, WPS);
   const int lane = threadIdx.x & (kWave - 1);
   const int wv = WPS > 1 ? __builtin_amdgcn_readfirstlane(threadIdx.x / kWave) : 0;
   const int g = lane >> 4;
   const int m16 = lane & 15;
   uint32_t* const stage = vst + wv * kVStage;           // this wave's V stage
+  uint32_t* const kstage = vst + (WPS + wv) * kVStage;  // its K stage (KST)
 
   // this tile's query positions: j0 .. j0 + jn - 1 of the sequence
   const int j0 = qt * p.qtile;
@@ -357,11 +374,21 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
     for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        if (FP8) {
+        if (KST && FP8) {
+          // whole lines, as V: FP8 row 8 s + lane / 8, bytes 16 (lane % 8) .. +15
+          if (kt == 0)
+            ch.k[0][s] = __builtin_bit_cast(
+                uint4, __builtin_amdgcn_raw_buffer_load_b128(kr, voff[s], 0, kLoadStreamed));
+        } else if (FP8) {
           const uint2 w = __builtin_bit_cast(
               uint2,
               __builtin_amdgcn_raw_buffer_load_b64(kr, koff[kt] + 32 * s, 0, 0));
           ch.k[kt][s] = make_uint4(w.x, w.y, 0, 0);
+        } else if (KST) {
+          // whole lines, as V: row 4 (4 kt + s) + g, bytes 16 m16 .. +15
+          ch.k[kt][s] = __builtin_bit_cast(
+              uint4,
+              __builtin_amdgcn_raw_buffer_load_b128(kr, voff[4 * kt + s], 0, kLoadStreamed));
         } else {
           ch.k[kt][s] = __builtin_bit_cast(
               uint4,
@@ -398,10 +425,28 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
         *reinterpret_cast<bf16x8_t*>(dst + (swap ? 4 : 0)) = fp8x8_to_bf16(swap ? hi : lo);
         *reinterpret_cast<bf16x8_t*>(dst + (swap ? 0 : 4)) = fp8x8_to_bf16(swap ? lo : hi);
       }
+      if (KST) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int row = 8 * i + (lane >> 3);
+          uint32_t* dst = kstage + row * kVPitch + (lane & 7) * 8;
+          const uint4 k = ch.k[0][i];
+          const uint2 lo = make_uint2(k.x, k.y), hi = make_uint2(k.z, k.w);
+          *reinterpret_cast<bf16x8_t*>(dst + (swap ? 4 : 0)) = fp8x8_to_bf16(swap ? hi : lo);
+          *reinterpret_cast<bf16x8_t*>(dst + (swap ? 0 : 4)) = fp8x8_to_bf16(swap ? lo : hi);
+        }
+        lds_wave_sync();
+      }
     } else {
 #pragma unroll
       for (int i = 0; i < 8; ++i)
         *reinterpret_cast<uint4*>(stage + (4 * i + g) * kVPitch + m16 * 4) = ch.v[i];
+      if (KST) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          *reinterpret_cast<uint4*>(kstage + (4 * i + g) * kVPitch + m16 * 4) = ch.k[i / 4][i % 4];
+        lds_wave_sync();
+      }
     }
 
     // ---- S^T = K . Q^T: per head_dim slice s, every (key tile, query
@@ -415,9 +460,14 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
     for (int s = 0; s < 4; ++s) {
       bf16x8_t kop[2];
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-        kop[kt] = FP8 ? fp8x8_to_bf16(make_uint2(ch.k[kt][s].x, ch.k[kt][s].y))
-                      : __builtin_bit_cast(bf16x8_t, ch.k[kt][s]);
+      for (int kt = 0; kt < 2; ++kt) {
+        if (KST)  // key 16 kt + m16, head_dim 32 s + 8 g .. +7 (the Q operands' order)
+          kop[kt] = *reinterpret_cast<const bf16x8_t*>(kstage + (16 * kt + m16) * kVPitch +
+                                                       4 * (4 * s + g));
+        else
+          kop[kt] = FP8 ? fp8x8_to_bf16(make_uint2(ch.k[kt][s].x, ch.k[kt][s].y))
+                        : __builtin_bit_cast(bf16x8_t, ch.k[kt][s]);
+      }
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         const bf16x8_t qo = qst[(nt * 4 + s) * kWave + lane];
@@ -735,7 +785,8 @@ template <int NT, bool FP8, bool PIPE, int WPS>
 __global__ void __launch_bounds__(kWave * WPS, NT >= 4 ? 1 : 2)
 paged_attention_kernel(AttnParams p) {
   // WPS V stages; shared segments park their states in NT banks of WPS stages
-  __shared__ __attribute__((aligned(16))) uint32_t vst[kVStage * WPS * (WPS > 1 && NT > 1 ? NT : 1)];
+  __shared__ __attribute__((aligned(16))) uint32_t
+      vst[kVStage * WPS * (k_staged(FP8, PIPE, WPS) ? 2 : (WPS > 1 && NT > 1 ? NT : 1))];
   __shared__ bf16x8_t qst[NT * 4 * kWave];
   const int kvh = blockIdx.x;
   const int row = blockIdx.y;
@@ -1079,7 +1130,7 @@ paged_attention_tile_kernel(AttnParams p) {
 template <int NT, bool FP8, bool PIPE>
 __global__ void __launch_bounds__(kWave, PIPE ? 1 : 2)
 paged_attention_stream_kernel(AttnParams p) {
-  __shared__ __attribute__((aligned(16))) uint32_t vst[kVStage];
+  __shared__ __attribute__((aligned(16))) uint32_t vst[kVStage * (k_staged(FP8, PIPE, 1) ? 2 : 1)];
   __shared__ bf16x8_t qst[NT * 4 * kWave];
   __shared__ int pre[kMaxSeqGroups * kWave + 1];          // pre[s]: chunks of sequences < s
   const int kvh = blockIdx.x;
@@ -1165,28 +1216,63 @@ paged_attention_stream_kernel(AttnParams p) {
 
 // Merge split partials.  Workgroup (t, y) merges, for token row t, the
 // 256 (head, 4-element) slices y*256 .. of the row; each thread owns one
-// slice.  The attention kernel recorded each row's split count, so a row
-// costs one dependent load before its partials; every thread issues the
-// loads of up to kCombineBatch splits at once (partials are laid out
-// [row][head][split][d]) and merges batches with a running log-sum-exp.
+// slice.  The attention kernel recorded each row's split count.  Partials
+// are laid out [row][head][split][d].  When the launch has at most
+// kCombineBatch splits per row (the fixed decomposition), every thread
+// issues the split count, the batch bounds and all max_splits log-sum-exps
+// and partials at once, whatever the count turns out to be (slots past it
+// hold an earlier call's values, or nothing meaningful, and are dropped):
+// one memory latency instead of two.  Otherwise (stream mode's longer
+// split lists) the count comes first and batches of kCombineBatch splits
+// follow, merged with a running log-sum-exp.
 constexpr int kCombineBatch = 8;
 __global__ void __launch_bounds__(kCombineThreads)
 combine_kernel(AttnParams p) {
   const int t = blockIdx.x;
   const int tid = threadIdx.x;
   if (t >= p.num_tokens) return;
-  // rows outside the batch's query range were not written by this call
-  const int lo = p.cu_q ? p.cu_q[0] : 0;
-  const int hi = p.cu_q ? p.cu_q[p.num_seqs] : p.num_seqs;
-  int nsplit = p.row_nsplit[t];
-  if (t < lo || t >= hi || nsplit <= 1) return;
-  nsplit = nsplit < p.max_splits ? nsplit : p.max_splits;
   const int idx = blockIdx.y * kCombineThreads + tid;
   if (idx >= p.hq * (kD / 4)) return;
   const int h = idx / (kD / 4), d4 = idx % (kD / 4);
   const int64_t base = (static_cast<int64_t>(t) * p.hq + h) * p.max_splits;
+  // rows outside the batch's query range were not written by this call
+  const int lo = p.cu_q ? p.cu_q[0] : 0;
+  const int hi = p.cu_q ? p.cu_q[p.num_seqs] : p.num_seqs;
+  int nsplit = p.row_nsplit[t];
   float M = -INFINITY, wsum = 0.0f;
   float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (p.max_splits <= kCombineBatch) {
+    float lse[kCombineBatch];
+    float4 v[kCombineBatch];
+#pragma unroll
+    for (int u = 0; u < kCombineBatch; ++u) {
+      if (u < p.max_splits) {
+        lse[u] = p.ws_lse[base + u];
+        v[u] = *reinterpret_cast<const float4*>(p.ws_o + (base + u) * kD + 4 * d4);
+      }
+    }
+    if (t < lo || t >= hi || nsplit <= 1) return;
+#pragma unroll
+    for (int u = 0; u < kCombineBatch; ++u)
+      if (u < p.max_splits && u < nsplit) M = fmaxf(M, lse[u]);
+    if (M != -INFINITY) {
+#pragma unroll
+      for (int u = 0; u < kCombineBatch; ++u) {
+        if (u < p.max_splits && u < nsplit) {
+          const float w = lse[u] == -INFINITY ? 0.0f : exp2f_fast(lse[u] - M);
+          wsum += w;
+          o.x += w * v[u].x; o.y += w * v[u].y; o.z += w * v[u].z; o.w += w * v[u].w;
+        }
+      }
+    }
+    const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
+    uint16_t* op = p.out + static_cast<int64_t>(t) * p.out_row_stride +
+                   static_cast<int64_t>(h) * p.out_head_stride + 4 * d4;
+    *reinterpret_cast<uint2*>(op) = make_uint2(pack_bf16(o.x * inv, o.y * inv), pack_bf16(o.z * inv, o.w * inv));
+    return;
+  }
+  if (t < lo || t >= hi || nsplit <= 1) return;
+  nsplit = nsplit < p.max_splits ? nsplit : p.max_splits;
   for (int s0 = 0; s0 < nsplit; s0 += kCombineBatch) {
     float lse[kCombineBatch];
     float4 v[kCombineBatch];
