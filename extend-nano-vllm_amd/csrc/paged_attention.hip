@@ -32,8 +32,13 @@
 //   * The MFMA sums over K in any order, so K and Q operands only have to
 //     agree on which head_dim element sits in which lane slot: lane l holds
 //     row (l % 16) and elements 32*s + 8*(l/16) .. +7 of slice s, a 16-byte
-//     load straight from the paged cache.  The Q operands are parked in LDS
-//     in that order and re-read per chunk, so they hold no registers.
+//     load straight from the paged cache, or (FP8 caches, and bf16 segments
+//     shared by several waves) a 16-byte read of a wave-private LDS tile
+//     that the K rows were staged into (XOR-swizzled 16-byte columns, see
+//     kst_slot), so that K too loads whole 128-byte lines with the
+//     non-temporal hint, as V does.  The Q operands
+//     are parked in LDS in that order and re-read per chunk, so they hold no
+//     registers.
 //   * The S^T accumulator layout (lane l: query column l % 16, keys
 //     4*(l/16) + i) is exactly the B-operand layout of the P^T operand once
 //     the 8 lane slots are mapped to keys {4g..4g+3, 16+4g..16+4g+3}; V^T uses
@@ -239,6 +244,14 @@ __device__ __forceinline__ int split_block_ids(const AttnParams& p, int seq, int
 #ifndef NVA_K_STAGE
 #define NVA_K_STAGE 1
 #endif
+// Dword offset of 16-byte column c (0..15) of K row r in a K stage: rows of
+// 64 dwords, the column XORed with the row's low four bits, so that the
+// 16 rows of an operand read (one column) and the 16 columns of a staging
+// write (one row) each fall on 16 different 16-byte bank groups.  With the
+// V stage's 68-dword pitch instead, the operand reads conflicted (626 k
+// conflict cycles per config-3 call, 10.5 M per FP8 config-4 call; 0 with
+// the swizzle, the call times unchanged).
+__device__ __forceinline__ int kst_slot(int r, int c) { return r * 64 + ((c ^ (r & 15)) << 2); }
 constexpr bool k_staged(bool fp8, bool pipe, int wps) {
   return NVA_K_STAGE && (fp8 || (!pipe && wps > 1));
 }
@@ -352,10 +365,16 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
   // previous chunk's math).  The descriptors' record count ends at the last
   // visible key, so rows past the sequence end (and every row of an invalid
   // block) read as zeros instead of stale cache contents.  V loads (whole
-  // 128-byte lines per instruction) carry the non-temporal hint; K loads
-  // (half lines per instruction, the other half one instruction later) do
-  // not.  Measured on the Qwen3-8B bench shapes: no hint 63.5 us per call,
-  // both 61.3, K only 63.7, V only 59.3; FP8 config 4: 486 -> 442 us.
+  // 128-byte lines per instruction) carry the non-temporal hint.  K loaded
+  // straight into operand order reads half lines per instruction (the
+  // other half one instruction later), where the hint costs time: measured
+  // on the Qwen3-8B bench shapes, no hint 63.5 us per call, both 61.3, K
+  // only 63.7, V only 59.3; FP8 config 4: 486 -> 442 us.  Staged K (KST)
+  // loads as V does, whole lines with the hint: config 3 56.4 -> 55.2 us,
+  // FP8 config 4 430.6 -> 414 us.  Issuing the next chunk's loads as soon
+  // as the staging frees the registers (before this chunk's math) ran
+  // slower, 55.2 -> 56.1 us: more requests in flight per CU, less DRAM
+  // efficiency.
   auto load_chunk = [&](int c, Chunk& ch) {
     const int kb = kv_begin + c * kChunk;
     ch.kb = kb;
@@ -429,11 +448,13 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int row = 8 * i + (lane >> 3);
-          uint32_t* dst = kstage + row * kVPitch + (lane & 7) * 8;
+          const int c0 = 2 * (lane & 7);
           const uint4 k = ch.k[0][i];
           const uint2 lo = make_uint2(k.x, k.y), hi = make_uint2(k.z, k.w);
-          *reinterpret_cast<bf16x8_t*>(dst + (swap ? 4 : 0)) = fp8x8_to_bf16(swap ? hi : lo);
-          *reinterpret_cast<bf16x8_t*>(dst + (swap ? 0 : 4)) = fp8x8_to_bf16(swap ? lo : hi);
+          *reinterpret_cast<bf16x8_t*>(kstage + kst_slot(row, c0 + (swap ? 1 : 0))) =
+              fp8x8_to_bf16(swap ? hi : lo);
+          *reinterpret_cast<bf16x8_t*>(kstage + kst_slot(row, c0 + (swap ? 0 : 1))) =
+              fp8x8_to_bf16(swap ? lo : hi);
         }
         lds_wave_sync();
       }
@@ -444,7 +465,7 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
       if (KST) {
 #pragma unroll
         for (int i = 0; i < 8; ++i)
-          *reinterpret_cast<uint4*>(kstage + (4 * i + g) * kVPitch + m16 * 4) = ch.k[i / 4][i % 4];
+          *reinterpret_cast<uint4*>(kstage + kst_slot(4 * i + g, m16)) = ch.k[i / 4][i % 4];
         lds_wave_sync();
       }
     }
@@ -462,8 +483,7 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt) {
         if (KST)  // key 16 kt + m16, head_dim 32 s + 8 g .. +7 (the Q operands' order)
-          kop[kt] = *reinterpret_cast<const bf16x8_t*>(kstage + (16 * kt + m16) * kVPitch +
-                                                       4 * (4 * s + g));
+          kop[kt] = *reinterpret_cast<const bf16x8_t*>(kstage + kst_slot(16 * kt + m16, 4 * s + g));
         else
           kop[kt] = FP8 ? fp8x8_to_bf16(make_uint2(ch.k[kt][s].x, ch.k[kt][s].y))
                         : __builtin_bit_cast(bf16x8_t, ch.k[kt][s]);
