@@ -1236,63 +1236,28 @@ paged_attention_stream_kernel(AttnParams p) {
 
 // Merge split partials.  Workgroup (t, y) merges, for token row t, the
 // 256 (head, 4-element) slices y*256 .. of the row; each thread owns one
-// slice.  The attention kernel recorded each row's split count.  Partials
-// are laid out [row][head][split][d].  When the launch has at most
-// kCombineBatch splits per row (the fixed decomposition), every thread
-// issues the split count, the batch bounds and all max_splits log-sum-exps
-// and partials at once, whatever the count turns out to be (slots past it
-// hold an earlier call's values, or nothing meaningful, and are dropped):
-// one memory latency instead of two.  Otherwise (stream mode's longer
-// split lists) the count comes first and batches of kCombineBatch splits
-// follow, merged with a running log-sum-exp.
+// slice.  The attention kernel recorded each row's split count, so a row
+// costs one dependent load before its partials; every thread issues the
+// loads of up to kCombineBatch splits at once (partials are laid out
+// [row][head][split][d]) and merges batches with a running log-sum-exp.
 constexpr int kCombineBatch = 8;
 __global__ void __launch_bounds__(kCombineThreads)
 combine_kernel(AttnParams p) {
   const int t = blockIdx.x;
   const int tid = threadIdx.x;
   if (t >= p.num_tokens) return;
-  const int idx = blockIdx.y * kCombineThreads + tid;
-  if (idx >= p.hq * (kD / 4)) return;
-  const int h = idx / (kD / 4), d4 = idx % (kD / 4);
-  const int64_t base = (static_cast<int64_t>(t) * p.hq + h) * p.max_splits;
   // rows outside the batch's query range were not written by this call
   const int lo = p.cu_q ? p.cu_q[0] : 0;
   const int hi = p.cu_q ? p.cu_q[p.num_seqs] : p.num_seqs;
   int nsplit = p.row_nsplit[t];
-  float M = -INFINITY, wsum = 0.0f;
-  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (p.max_splits <= kCombineBatch) {
-    float lse[kCombineBatch];
-    float4 v[kCombineBatch];
-#pragma unroll
-    for (int u = 0; u < kCombineBatch; ++u) {
-      if (u < p.max_splits) {
-        lse[u] = p.ws_lse[base + u];
-        v[u] = *reinterpret_cast<const float4*>(p.ws_o + (base + u) * kD + 4 * d4);
-      }
-    }
-    if (t < lo || t >= hi || nsplit <= 1) return;
-#pragma unroll
-    for (int u = 0; u < kCombineBatch; ++u)
-      if (u < p.max_splits && u < nsplit) M = fmaxf(M, lse[u]);
-    if (M != -INFINITY) {
-#pragma unroll
-      for (int u = 0; u < kCombineBatch; ++u) {
-        if (u < p.max_splits && u < nsplit) {
-          const float w = lse[u] == -INFINITY ? 0.0f : exp2f_fast(lse[u] - M);
-          wsum += w;
-          o.x += w * v[u].x; o.y += w * v[u].y; o.z += w * v[u].z; o.w += w * v[u].w;
-        }
-      }
-    }
-    const float inv = wsum > 0.0f ? 1.0f / wsum : 0.0f;
-    uint16_t* op = p.out + static_cast<int64_t>(t) * p.out_row_stride +
-                   static_cast<int64_t>(h) * p.out_head_stride + 4 * d4;
-    *reinterpret_cast<uint2*>(op) = make_uint2(pack_bf16(o.x * inv, o.y * inv), pack_bf16(o.z * inv, o.w * inv));
-    return;
-  }
   if (t < lo || t >= hi || nsplit <= 1) return;
   nsplit = nsplit < p.max_splits ? nsplit : p.max_splits;
+  const int idx = blockIdx.y * kCombineThreads + tid;
+  if (idx >= p.hq * (kD / 4)) return;
+  const int h = idx / (kD / 4), d4 = idx % (kD / 4);
+  const int64_t base = (static_cast<int64_t>(t) * p.hq + h) * p.max_splits;
+  float M = -INFINITY, wsum = 0.0f;
+  float4 o = make_float4(0.f, 0.f, 0.f, 0.f);
   for (int s0 = 0; s0 < nsplit; s0 += kCombineBatch) {
     float lse[kCombineBatch];
     float4 v[kCombineBatch];
