@@ -1065,6 +1065,13 @@ def forced_acceptance(args, tmp: str, continuations):
                 mean_acceptance_length=round(wst["committed"] / max(wst["steps"] * n_active, 1),
                                              4)),
             "outputs_equal_main_run": f"{same} of {len(prompts)}",
+            "outputs_equal_note": (
+                "the forced run's batch shrinks as its sequences finish, so its later verify "
+                "steps run with other GEMM row counts and, below 33 sequences, another verify-"
+                "attention decomposition (eight waves per split instead of paired mode), whose "
+                "last-bit rounding differs; sequences that part from the main run do so where "
+                "that rounding flips a near tie (with either decomposition forced for every "
+                "batch size, 63 of 64 sequences equal)"),
             "drafts": "target-greedy continuation of each sequence (recorded by the main run, "
                       "whose steps commit exactly the target's argmax), kept per position with "
                       "probability draft_keep"}
