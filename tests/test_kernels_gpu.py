@@ -455,6 +455,21 @@ def test_verify_attention_fp8(K, cuda):
     assert err <= ATTN_TOL, err
 
 
+@pytest.mark.parametrize("name,kw", [
+    # more sequences than the stream decomposition takes (8 x 64): the fixed
+    # FP8 path with its K rows staged, 4-row tiles (one column tile) and
+    # 20-row tiles (two); 32-token pages keep the cache small
+    ("fp8_fixed_4rows", dict(seed=40, batch=520, q_len=2, ctx_lo=2, ctx_hi=100, hq=4, hkv=2,
+                             block_size=32)),
+    ("fp8_fixed_20rows", dict(seed=41, batch=520, q_len=5, ctx_lo=5, ctx_hi=100, hq=8, hkv=2,
+                              block_size=32)),
+])
+def test_verify_attention_fp8_fixed_decomposition(K, cuda, name, kw):
+    got, ref = _run_verify(K, cuda, paged_case(**kw), fp8=True)
+    err = np.abs(got - ref).max()
+    assert err <= ATTN_TOL, (name, err)
+
+
 @pytest.mark.parametrize("pages", ["head_major", "kv_adjacent"])
 @pytest.mark.parametrize("fp8", [False, True])
 @pytest.mark.parametrize("name,kw", [
