@@ -13,7 +13,7 @@
 //     the same number of keys whatever the length mix;
 //   * fixed (everything else): one workgroup per (kv head, sequence, query
 //     tile, key split).  For bf16 tiles of up to 32 rows eight waves share a
-//     2688-key split (wave w takes chunks w, w+8, ...) and fold their
+//     2816-key split (wave w takes chunks w, w+8, ...) and fold their
 //     softmax states together in LDS; for single-tile 17-32-row tiles whose
 //     segments fill every CU once or twice, four waves share a whole
 //     sequence instead and the grid pairs a long sequence with a short one
@@ -71,7 +71,7 @@ constexpr int kChunk = 32;
 constexpr int kVPitch = 68;                          // dwords per staged V row
 constexpr int kVStage = kChunk * kVPitch;            // dwords of the wave's V stage
 constexpr int kSplitKeys = 3072;       // fixed decomposition, one wave per split
-constexpr int kKeysPerSharedWave = 336; // fixed decomposition, several waves per split
+constexpr int kKeysPerSharedWave = 352; // fixed decomposition, several waves per split
 constexpr int kMinSplit = 128;
 constexpr int64_t kMinWaves = 1024;
 // a split spans at most kWave - 2 blocks; blocks hold at least kChunk tokens
@@ -1314,8 +1314,8 @@ int32_t device_cus() {
 
 // Split length of the fixed decomposition.  A segment is one (sequence, kv
 // head, query tile); `waves` waves share each split.
-//   * Eight waves per split (bf16 tiles of up to 32 rows): 336 keys per
-//     wave, 2688 per split; when the batch has at least four segments per
+//   * Eight waves per split (bf16 tiles of up to 32 rows): 352 keys per
+//     wave, 2816 per split; when the batch has at least four segments per
 //     CU (several rounds of workgroups, which the dispatcher balances), one
 //     split covers the whole sequence instead (no fp32 partials, no
 //     combine, each workgroup streams longer).
@@ -1332,7 +1332,10 @@ int32_t device_cus() {
 // at 2688, 58.4-58.5 at 2816, 59.6 at 2560, 60.1-60.9 at 3072, 61.5-62.4 at
 // 2304, 64.4 at 2048, 64.3 whole: in one round the split balances the
 // longest first splits against a short sequence plus the longest second
-// split, each workgroup's start-up worth ~340 keys of streaming.  The length shrinks in 128-key steps (to a 128-key
+// split, each workgroup's start-up worth ~340 keys of streaming.  With K
+// staged through LDS (two alternating sweeps on one box): 55.2-55.3 at
+// 2816, 55.6-55.7 at 2944, 55.8-55.9 at 2688, 56.5 at 2560 and at 3072,
+// 56.6 at 2432.  The length shrinks in 128-key steps (to a 128-key
 // minimum) only while fewer than kMinWaves waves would be launched, and is
 // capped so that a split spans at most kWave - 2 blocks of block_size tokens
 // (the kernel holds one block id per lane); block_size 0 (unknown: the
