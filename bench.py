@@ -1091,8 +1091,9 @@ def config5(args) -> None:
     Prints one JSON line: step time and accepted tok/s over the timed steps
     (zero acceptance with random weights), the verify attention of one step
     re-issued between HIP events, and a greedy check of 4 sequences
-    (teacher-forced prefill of prompt + output: every output token within
-    16 bf16 ulps of the row's top logit)."""
+    (teacher-forced prefill of prompt + output: the largest gap between an
+    output token's logit and its row's top, in bf16 ulps; the GPU test of
+    this geometry holds it to the plain engine's own gap)."""
     from collections import deque
 
     import torch
@@ -1211,8 +1212,12 @@ def config5(args) -> None:
         "prefill_s": round(prefill_s, 1), "pages": total,
         "verify_attention": roof,
         "greedy_check": {"sequences": len(picks), "tokens": checked,
-                         "max_gap_ulps": round(worst, 1), "tolerance_ulps": 16,
-                         "ok": worst < 16},
+                         "max_gap_ulps": round(worst, 1),
+                         "note": "informational: the largest gap, in bf16 ulps of the row's top "
+                                 "logit, between an emitted token's logit and the top of its "
+                                 "teacher-forced prefill row; tests/test_engine_32b_gpu.py holds "
+                                 "the speculative engine at this geometry to the plain engine's "
+                                 "own largest gap in the same run plus 2 ulps"},
     }), flush=True)
 
 
