@@ -9,26 +9,32 @@ The logits are bf16.  At these geometries the top logits sit near 6, where
 one bf16 ulp is 2^-5 = 0.031, so an absolute 2e-2 margin would only excuse
 exact ties, while two bf16 computations of the same logits by different
 paths (the plain engine's one-row decode, the verify's k+1 rows, a prefill
-over the whole sequence) differ by a few ulps.  So the tolerance is measured
+over the whole sequence) differ by a few ulps.  So the bounds are measured
 in the same run, from a control: the non-speculative engine's own tokens
 are compared with the argmax of a teacher-forced prefill of prompt + output,
-and the largest gap (in bf16 ulps of the row's top logit) is the smallest
-tolerance the plain engine itself passes.  The speculative engine is a
-second bf16 path of the same accuracy, so its gaps are a second sample of
-the same distribution, and the two samples' maxima differ by a couple of
-ulps (measured at config 3, 16384 tokens each: histograms alike bin for
-bin, 1564 against 1566 tokens below the top, maxima 9 and 11; at config 5:
-maxima 9 and 10).  So the tolerance is the control's maximum plus
-SLACK_ULPS = 2, and the speculative engine is held to it:
+and each token's gap (in bf16 ulps of the row's top logit) is recorded.
+The speculative engine is a second bf16 path of the same accuracy, so its
+gaps are a second sample of the same distribution (measured at config 3,
+16384 tokens each: histograms alike bin for bin, 1564 against 1566 tokens
+below the top).  The checks compare the two samples:
 
-* at the first position where its output parts from the plain engine's, the
-  two tokens' logits (prefill of the common prefix) differ by at most the
-  tolerance (a near tie, broken differently by the two paths);
-* every token it emits, after the parting point too, sits at most the
-  tolerance below its prefill row's top logit (a greedy path of its own);
 * the number of its tokens below the top differs from the control's by at
   most four Poisson standard deviations (a path that is slightly off moves
-  many near ties, not only the largest gap).
+  many near ties, not only the largest gap);
+* the tail: its 99th-percentile gap is at most TAIL_SLACK_ULPS = 3 above
+  the control's.  An order statistic that deep (the ~15th largest of ~1500
+  tokens) moves by about an ulp between two samples of one distribution,
+  where the samples' maxima do not hold still: the gap histograms decay by
+  about x0.7 per ulp, so two maxima differ by more than 2 ulps in about a
+  third of runs (maxima 9 and 11 at config 3; 9 and 10, and 10 and 13 in
+  another run, at config 5);
+* every token it emits, after a parting point too, sits at most
+  2 x (the control's largest gap) + 2 ulps below its prefill row's top
+  logit (a greedy path of its own: one token beyond twice the control's
+  worst would be no near tie), and so does the margin between the two
+  tokens at each position where its output first parts from the plain
+  engine's (a near tie broken differently by the two paths: that margin is
+  never more than one of the two engines' own gaps at the position).
 
 A token from a broken path sits ~5 logit standard deviations (~200 ulps)
 below the top.  With random weights the draft agrees with the target at
@@ -51,7 +57,15 @@ from nanovllm_amd.context import reset_context
 from nanovllm_amd.engine.sequence import Sequence
 
 KEEP = 0.7
-SLACK_ULPS = 2.0
+SLACK_ULPS = 2.0          # over twice the control's largest gap
+TAIL_SLACK_ULPS = 3.0     # over the control's 99th-percentile gap
+
+
+def tail_gap(gaps: list[float]) -> float:
+    """The 99th-percentile gap: the (n // 100)-th largest (at least the
+    largest)."""
+    ordered = sorted(gaps, reverse=True)
+    return ordered[max(len(ordered) // 100, 1) - 1]
 
 
 def release(llm) -> None:
@@ -119,10 +133,12 @@ def run(make_llm, prompts, k: int, max_tokens: int, tag: str, page_seed: int | N
     finally:
         release(plain)
     flat = [g for c in control for g in c]
-    tol = max(flat) + SLACK_ULPS
+    tol = 2 * max(flat) + SLACK_ULPS
+    tail_tol = tail_gap(flat) + TAIL_SLACK_ULPS
     print(f"[{tag}] plain engine: {sum(g > 0 for g in flat)} of {len(flat)} tokens below the "
-          f"prefill's top logit, at most {max(flat):.1f} ulps -> tolerance {tol:.1f} ulps",
-          flush=True)
+          f"prefill's top logit, at most {max(flat):.1f} ulps, 99th percentile "
+          f"{tail_gap(flat):.1f} -> bounds: every token {tol:.1f} ulps, 99th percentile "
+          f"{tail_tol:.1f} ulps", flush=True)
 
     full = {tuple(p): p + r for p, r in zip(prompts, ref)}
     spec = make_llm(spec=True)
@@ -182,19 +198,23 @@ def run(make_llm, prompts, k: int, max_tokens: int, tag: str, page_seed: int | N
     print(f"[{tag}] gap histogram (ulps: tokens) spec  {hist(flat_own)}", flush=True)
     print(f"[{tag}] speculative engine: stats {stats}, forced steps {forced}; "
           f"{sum(g > 0 for g in flat_own)} of {len(flat_own)} tokens below the prefill's top "
-          f"logit, at most {max(flat_own):.1f} ulps", flush=True)
+          f"logit, at most {max(flat_own):.1f} ulps, 99th percentile {tail_gap(flat_own):.1f}",
+          flush=True)
     print(f"[{tag}] {len(parts)} of {batch} sequences part from the plain engine; "
           f"(sequence, position, margin in ulps): "
           f"{[(i, n, round(m, 1)) for i, n, m in parts]}", flush=True)
     below_plain = sum(g > 0 for g in flat)
     below_spec = sum(g > 0 for g in flat_own)
-    summary = {"tolerance_ulps": tol, "plain_max_ulps": max(flat), "spec_max_ulps": max(flat_own),
+    summary = {"tolerance_ulps": tol, "tail_tolerance_ulps": tail_tol,
+               "plain_max_ulps": max(flat), "spec_max_ulps": max(flat_own),
+               "plain_tail_ulps": tail_gap(flat), "spec_tail_ulps": tail_gap(flat_own),
                "below_top": (below_plain, below_spec), "parting": parts, "stats": stats,
                "forced": forced}
     # the checks
     for out in got:
         assert len(out) == max_tokens
     assert abs(below_spec - below_plain) <= 4 * below_plain ** 0.5 + 4, (below_plain, below_spec)
+    assert tail_gap(flat_own) <= tail_tol, (tail_gap(flat), tail_gap(flat_own))
     worst = [(i, j, round(g, 1)) for i, c in enumerate(own) for j, g in enumerate(c) if g > tol]
     assert not worst, f"tokens more than {tol:.1f} ulps below the top logit: {worst[:20]}"
     wide = [(i, n, round(m, 1)) for i, n, m in parts if m > tol]
