@@ -283,7 +283,7 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
   const int g = lane >> 4;
   const int m16 = lane & 15;
   uint32_t* const stage = vst + wv * kVStage;           // this wave's V stage
-  uint32_t* const kstage = vst + (WPS + wv) * kVStage;  // its K stage (KST)
+  uint32_t* const kstage = KST ? vst + (WPS + wv) * kVStage : stage;  // its K stage
 
   // this tile's query positions: j0 .. j0 + jn - 1 of the sequence
   const int j0 = qt * p.qtile;
@@ -804,7 +804,8 @@ __device__ __forceinline__ int stream_chunks(const AttnParams& p, int seq) {
 template <int NT, bool FP8, bool PIPE, int WPS>
 __global__ void __launch_bounds__(kWave * WPS, NT >= 4 ? 1 : 2)
 paged_attention_kernel(AttnParams p) {
-  // WPS V stages; shared segments park their states in NT banks of WPS stages
+  // WPS V stages, then WPS K stages where K is staged; shared segments park
+  // their states in NT banks of WPS stages (the second bank is the K stages)
   __shared__ __attribute__((aligned(16))) uint32_t
       vst[kVStage * WPS * (k_staged(FP8, PIPE, WPS) ? 2 : (WPS > 1 && NT > 1 ? NT : 1))];
   __shared__ bf16x8_t qst[NT * 4 * kWave];
