@@ -501,7 +501,21 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
     // running max m_run (scaled, log2 domain) is only raised when a column's
     // new max exceeds it by more than kRescaleSlack, so the accumulator
     // rescale is skipped for most chunks: probabilities stay <= 2^kRescaleSlack.
+    // Only a chunk that reaches past some column's causal limit (or the
+    // sequence end) is masked, behind a uniform branch: written as a select
+    // per score, the compare and select ran on every chunk (40 VALU
+    // instructions of ~170 per chunk).
     const bool full = kb + kChunk - 1 <= L - q_len + j0 && kb + kChunk <= kv_limit;
+    if (!full) {
+      const int rel = kb + 4 * g;
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (rel + kt * 16 + i > lim[nt]) sacc[kt][nt][i] = -INFINITY;
+    }
     bf16x8_t pb[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) {
@@ -511,8 +525,7 @@ __device__ __forceinline__ void attend_segment(const AttnParams& p, uint32_t* vs
       for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float v = sacc[kt][nt][i];
-          if (!full) v = (kb + kt * 16 + 4 * g + i <= lim[nt]) ? v : -INFINITY;
+          const float v = sacc[kt][nt][i];
           sv[kt * 4 + i] = v;
           cmax = fmaxf(cmax, v);
         }
@@ -1003,7 +1016,18 @@ paged_attention_tile_kernel(AttnParams p) {
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt) sacc[kt][nt] = mfma(kop[kt], qv[nt][s], sacc[kt][nt]);
     }
+    // masked only past a causal limit, behind a uniform branch (as above)
     const bool full = kb + kChunk - 1 <= L - q_len + j0 && kb + kChunk <= kv_limit;
+    if (!full) {
+      const int rel = kb + 4 * g;
+#pragma unroll
+      for (int nt = 0; nt < NTW; ++nt)
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (rel + kt * 16 + i > lim[nt]) sacc[kt][nt][i] = -INFINITY;
+    }
     bf16x8_t pb[NTW];
 #pragma unroll
     for (int nt = 0; nt < NTW; ++nt) {
@@ -1013,8 +1037,7 @@ paged_attention_tile_kernel(AttnParams p) {
       for (int kt = 0; kt < 2; ++kt) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          float v = sacc[kt][nt][i];
-          if (!full) v = (kb + kt * 16 + 4 * g + i <= lim[nt]) ? v : -INFINITY;
+          const float v = sacc[kt][nt][i];
           sv[kt * 4 + i] = v;
           cmax = fmaxf(cmax, v);
         }
