@@ -59,7 +59,7 @@ PMC_WORKLOAD = dict(preset="qwen3-8b", batch=64, k=5, prompt_min=256, prompt_max
 # the kernel source the counters were read on (sha256 of csrc/paged_attention.hip
 # then csrc/common.h, first 16 hex digits): the constant is quoted only while
 # the source is unchanged, since a change of the kernel's loads changes it
-PMC_ATTENTION_SOURCE = "f11861eb4bbc36b3"
+PMC_ATTENTION_SOURCE = "50d5b572de54e22a"
 ATTENTION_SOURCES = ("paged_attention.hip", "common.h")
 
 

@@ -44,7 +44,9 @@
 //     the 8 lane slots are mapped to keys {4g..4g+3, 16+4g..16+4g+3}; V^T uses
 //     the same key mapping.  V is therefore staged through a wave-private LDS
 //     tile (row pitch 68 dwords: conflict-free for the column reads) and read
-//     back two head_dim elements per dword, feeding an even and an odd d-tile.
+//     back two head_dim elements per dword, feeding an even and an odd d-tile;
+//     the shared-tile kernel instead reads its V^T operands with the LDS
+//     transpose load from 72-dword rows (v_operand_tr).
 //   * K/V loads are raw buffer loads from a per-chunk descriptor (uniform
 //     base, loop-invariant lane offsets, record count ending at the last
 //     visible key so that rows past it read as zeros).  Where a SIMD holds
