@@ -895,9 +895,9 @@ paged_attention_kernel(AttnParams p) {
 //     chunks ahead of the one being computed, into registers.  That keeps
 //     D * 16 KiB in flight per workgroup where one wave per SIMD holding
 //     all 64 columns' accumulators had room for one chunk ahead.
-//   * A chunk's registers are written to one of two LDS slots (K rows, then
-//     V rows, 68 dwords per row: conflict-free for the 16-byte writes, the
-//     16-byte K operand reads and the V column reads), and one barrier per
+//   * A chunk's registers are written to one of two LDS slots (K rows of 68
+//     dwords, conflict-free for the 16-byte writes and K operand reads, then
+//     V rows of 72 dwords for the transpose loads), and one barrier per
 //     chunk publishes it and frees the other slot.
 //   * The query operands stay in registers (NTW column tiles per wave); the
 //     S^T, softmax and O^T steps are attend_segment's, per wave.
@@ -1428,11 +1428,14 @@ void choose_split(int32_t num_seqs, int32_t num_kv_heads, int32_t n_qtiles, int3
 //   * single-tile sequences of up to 32 rows, FP8: stream decomposition with
 //     the chunk loads issued one chunk ahead (502 us against 573 us fixed);
 //   * bf16 64-row tiles: the shared-tile kernel, four waves per tile with
-//     every chunk loaded once per workgroup and two or three chunks in
-//     flight (Qwen3-32B verify, config 5's shapes: 425-428 us against 477 us
-//     for one wave per SIMD holding all 64 columns and one chunk ahead;
-//     four chunks in flight 441 us, the registers then allow two waves per
-//     SIMD instead of three; two waves per tile 432 us);
+//     every chunk loaded once per workgroup and four chunks in flight
+//     (Qwen3-32B verify, config 5's shapes: 425-428 us against 477 us for
+//     one wave per SIMD holding all 64 columns and one chunk ahead, when
+//     three chunks were in flight; four then took 441 us at 171 VGPRs, two
+//     waves per SIMD instead of three; with V through the LDS transpose
+//     load the kernel holds 151 / 160 VGPRs at three / four chunks, three
+//     waves per SIMD either way, and four chunks run 404-405 against 407 us;
+//     two waves per tile 432 us);
 //   * FP8 64-row tiles: fixed decomposition with the loads one chunk ahead
 //     (one wave per SIMD for 64 rows: no room for a second).
 // NVA_ATTN_STREAM=0/1 (1: also bf16 tiles of up to 16 rows) and
@@ -1556,7 +1559,7 @@ struct TileChoice {
 };
 TileChoice tile_choice() {
   static const TileChoice c = [] {
-    TileChoice t{4, 3};
+    TileChoice t{4, 4};
     const char* v = getenv("NVA_ATTN_TILE");
     if (v) {
       int w = 0, d = 0;
@@ -1575,18 +1578,18 @@ template <int WPT>
 void launch_tile(const AttnParams& p, int depth, dim3 grid, hipStream_t s) {
   if constexpr (WPT == 2) {
     paged_attention_tile_kernel<2, 2><<<grid, kWave * 2, 0, s>>>(p);
-    return;
-  }
-  switch (depth) {
-    case 3:
-      paged_attention_tile_kernel<WPT, 3><<<grid, kWave * WPT, 0, s>>>(p);
-      return;
-    case 4:
-      paged_attention_tile_kernel<WPT, 4><<<grid, kWave * WPT, 0, s>>>(p);
-      return;
-    default:
-      paged_attention_tile_kernel<WPT, 2><<<grid, kWave * WPT, 0, s>>>(p);
-      return;
+  } else {
+    switch (depth) {
+      case 3:
+        paged_attention_tile_kernel<WPT, 3><<<grid, kWave * WPT, 0, s>>>(p);
+        return;
+      case 4:
+        paged_attention_tile_kernel<WPT, 4><<<grid, kWave * WPT, 0, s>>>(p);
+        return;
+      default:
+        paged_attention_tile_kernel<WPT, 2><<<grid, kWave * WPT, 0, s>>>(p);
+        return;
+    }
   }
 }
 
